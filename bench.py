@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fp32 GEMM path (one JSON line on stdout).
+
+Headline (BASELINE.json metric): fp32 GEMM TFLOP/s at M = N = K = 4096,
+row-major NN, A and B ~ N(0, 1), as a fraction of the MI355X fp32-MFMA peak.
+A "step" is one GEMM launch over the resident operands.  The 784-256-10 MLP
+training step rate is reported beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--sweep FILE]
+
+Timing: W untimed launches, then K launches bracketed by
+torch.cuda.synchronize() with HIP events recorded on the stream the kernels
+are launched on (torch's current stream, whose handle is passed to the C-ABI).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix peak (256 CU x 256 FLOP/clk x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sgemm_nn_4096_traffic.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--size", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the MLP step rate")
+    ap.add_argument("--sweep", default=None, help="write every BASELINE config's timing here")
+    ap.add_argument("--profile-mode", action="store_true",
+                    help="only the headline launches (for rocprofv3 runs)")
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+    return float(m.group(1)) if m else None
+
+
+def time_launches(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per launch
+
+
+def gemm_case(capi, torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1):
+    """Resident operands and a launcher closure for one GEMM configuration.
+
+    rotate > 1 cycles through that many copies of the operands so the working
+    set exceeds the 256 MB Infinity Cache (HBM-bound shapes).
+    """
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    a_shape = (batch, K, M) if ta else (batch, M, K)
+    b_shape = (batch, N, K) if tb else (batch, K, N)
+    As = [torch.randn(a_shape, generator=gen, device="cuda") for _ in range(rotate)]
+    Bs = [torch.randn(b_shape, generator=gen, device="cuda") for _ in range(rotate)]
+    Cs = [torch.empty((batch, M, N), device="cuda") for _ in range(rotate)]
+    bias = torch.randn((N,), generator=gen, device="cuda") * 0.1
+    lda = M if ta else K
+    ldb = K if tb else N
+    stream = torch.cuda.current_stream().cuda_stream
+    state = {"i": 0}
+
+    def launch():
+        i = state["i"]
+        state["i"] = (i + 1) % rotate
+        capi.sgemm_ex(ta, tb, M, N, K, As[i].data_ptr(), lda, M * K, Bs[i].data_ptr(), ldb,
+                      K * N, Cs[i].data_ptr(), N, M * N, batch,
+                      bias.data_ptr() if epi in (1, 2) else None, None, epi, stream)
+
+    return launch, As[0], Bs[0], Cs[0]
+
+
+def cpu_baseline(n, rows):
+    """Restated reference CPU loop (oracle/gemm_cpu, 1 thread) on a row block."""
+    import numpy as np
+
+    import oracle
+
+    g = np.random.default_rng(0)
+    A = g.standard_normal((rows, n)).astype(np.float32)
+    B = g.standard_normal((n, n)).astype(np.float32)
+    t0 = time.perf_counter()
+    oracle.gemm_cpu(A, B)
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * n * n
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows} of {n} rows of the {n}^3 NN GEMM (gemm_cpu loop, gcc -O2, 1 thread), "
+                  f"{dt:.2f} s",
+    }
+
+
+def mlp_rate(capi, torch, steps=200, warmup=20):
+    """fdl_mlp2_train_step on BASELINE config 2 (784-256-10, batch 256), steps/s."""
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    B, I, H, C = 256, 784, 256, 10
+    X = torch.rand((B, I), generator=gen, device="cuda")
+    labels = torch.randint(0, C, (B,), generator=gen, device="cuda", dtype=torch.int64)
+    W1 = (torch.rand((I, H), generator=gen, device="cuda") * 2 - 1) * (6 / I) ** 0.5
+    W2 = (torch.rand((H, C), generator=gen, device="cuda") * 2 - 1) * (6 / H) ** 0.5
+    b1 = torch.zeros(H, device="cuda")
+    b2 = torch.zeros(C, device="cuda")
+    buf = {k: torch.empty(s, device="cuda") for k, s in dict(
+        H=(B, H), logits=(B, C), G2=(B, C), G1=(B, H), dW1=(I, H), db1=(H,), dW2=(H, C),
+        db2=(C,), dX=(B, I), loss=(1,)).items()}
+    stream = torch.cuda.current_stream().cuda_stream
+    p = {k: v.data_ptr() for k, v in buf.items()}
+    args = (X.data_ptr(), labels.data_ptr(), B, I, H, C, W1.data_ptr(), b1.data_ptr(),
+            W2.data_ptr(), b2.data_ptr(), 0.1, p["H"], p["logits"], p["G2"], p["G1"], p["dW1"],
+            p["db1"], p["dW2"], p["db2"], p["dX"], p["loss"], stream)
+
+    def step():
+        capi.mlp2_train_step(*args)
+
+    ms = time_launches(step, steps, warmup, torch.cuda.current_stream())
+    return 1000.0 / ms, ms, float(buf["loss"].item())
+
+
+def sampled_parity(A, B, C, n, rows=16):
+    """Cheap parity guard on the benchmarked output: sampled rows vs fp64 dot products."""
+    import numpy as np
+
+    import torch
+
+    torch.cuda.synchronize()
+    idx = torch.randint(0, n, (rows,), generator=torch.Generator().manual_seed(5))
+    a = A[0][idx.cuda()].double().cpu().numpy()
+    b = B[0].double().cpu().numpy()
+    c = C[0][idx.cuda()].double().cpu().numpy()
+    ref = a @ b
+    bound = 2.0 * (np.sqrt(n) + 2.0) * float(np.finfo(np.float32).eps) * (np.abs(a) @ np.abs(b))
+    return bool(np.all(np.abs(c - ref) <= bound))
+
+
+def sweep(capi, torch, path):
+    """Every BASELINE configuration, one line each (for DESIGN.md / profiles)."""
+    out = []
+
+    def rec(name, launch, flops, nbytes, steps=30, warmup=5):
+        ms = time_launches(launch, steps, warmup, torch.cuda.current_stream())
+        t = ms / 1e3
+        ridge = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+        bound = "mfma" if flops / nbytes >= ridge else "hbm"
+        row = {"config": name, "ms": ms, "tflops": flops / t / 1e12, "gbs": nbytes / t / 1e9,
+               "bound": bound,
+               "frac": (flops / t / 1e12 / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma"
+               else (nbytes / t / 1e9 / PEAK_HBM_GBS)}
+        out.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+
+    def b4(M, N, K, batch=1, bias=False):
+        return 4.0 * batch * (M * K + K * N + M * N) + (4.0 * N if bias else 0.0)
+
+    launch, *_ = gemm_case(capi, torch, 256, 128, 784)
+    rec("C1 256x128x784 NN", launch, 2.0 * 256 * 128 * 784, b4(256, 128, 784))
+    for n in (1024, 2048, 4096, 8192):
+        launch, *_ = gemm_case(capi, torch, n, n, n)
+        rec(f"C3 {n}^3 NN", launch, 2.0 * n ** 3, b4(n, n, n), steps=10 if n == 8192 else 30)
+    for tb in (0, 1):
+        launch, *_ = gemm_case(capi, torch, 128, 128, 64, tb=tb, batch=64, rotate=40)
+        rec(f"C4 64x(128x128x64) {'NT' if tb else 'NN'}", launch, 2.0 * 64 * 128 * 128 * 64,
+            b4(128, 128, 64, 64))
+    for m in (1, 8):
+        launch, *_ = gemm_case(capi, torch, m, 4096, 4096, epi=2, rotate=6)
+        rec(f"C5a M={m} K=N=4096 bias+relu", launch, 2.0 * m * 4096 * 4096,
+            b4(m, 4096, 4096, bias=True))
+    for n in (777, 1000, 1023):
+        launch, *_ = gemm_case(capi, torch, n, n, n, epi=2)
+        rec(f"C5b {n}^3 bias+relu", launch, 2.0 * n ** 3, b4(n, n, n, bias=True))
+    sps, ms, _ = mlp_rate(capi, torch)
+    out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps})
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path's multi-GPU sharding is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import fast_dl_amd.capi as capi
+
+    capi.load_library()
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    n = args.size
+    launch, A, B, C = gemm_case(capi, torch, n, n, n, seed=0)
+    stream = torch.cuda.current_stream()
+    ms = time_launches(launch, args.steps, args.warmup, stream)
+    if args.profile_mode:
+        print(json.dumps({"profile_mode": True, "ms_per_launch": ms}), flush=True)
+        return
+    flops = 2.0 * n * n * n
+    tflops = flops / (ms / 1e3) / 1e12
+    parity = sampled_parity(A, B, C, n)
+
+    mlp = None
+    if not args.no_mlp:
+        sps, mlp_ms, loss = mlp_rate(capi, torch)
+        mlp = {"steps_per_s": sps, "ms_per_step": mlp_ms, "final_loss": loss,
+               "config": "784-256-10, batch 256, lr 0.1, fdl_mlp2_train_step (dX included)"}
+    if args.sweep:
+        sweep(capi, torch, args.sweep)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(n, rows=32)
+
+    kernel = capi.KERNEL_NAMES.get(capi.kernel_choice(0, 0, n, n, n), "auto")
+    line = {
+        "metric": "fp32 GEMM TFLOP/s at M=N=K=4096 (% MI355X fp32 peak); MLP train steps/s",
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (torch.randn on device, seed 0)",
+        "config": {"workload": f"sgemm NN row-major M=N=K={n}, A,B ~ N(0,1)",
+                   "kernel": f"sgemm_tiled_kernel ({kernel})", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tflops / PEAK_FP32_MFMA_TFLOPS,
+                     "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "mlp_train": mlp,
+        "parity_sampled_rows_fp64": parity,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,121 @@
+"""ctypes binding of ``include/fastdl_gemm.h``.
+
+Every function takes raw device addresses (ints, e.g. ``tensor.data_ptr()``)
+and a raw ``hipStream_t`` (int, e.g. ``torch.cuda.current_stream().cuda_stream``,
+0 for the null stream).  Non-zero statuses raise :class:`FdlError` carrying
+the library's own message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+OP_N, OP_T = 0, 1
+EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_BIAS_RELU, EPILOGUE_RELU, EPILOGUE_RELU_GRAD = range(5)
+KERNEL_AUTO, KERNEL_TILED128, KERNEL_TILED64, KERNEL_SPLITK32, KERNEL_SKINNY = -1, 0, 1, 2, 3
+KERNEL_NAMES = {KERNEL_TILED128: "tiled128", KERNEL_TILED64: "tiled64",
+                KERNEL_SPLITK32: "splitk32", KERNEL_SKINNY: "skinny"}
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_flt = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/fastdl_gemm.h.
+SIGNATURES = {
+    "fdl_sgemm_ex": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                            _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
+    "fdl_sgemm_ex_select": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                                   _i64, _vp, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp]),
+    "fdl_sgemm_kernel_choice": (_int, [_int, _int, _i64, _i64, _i64, _i64]),
+    "fdl_gemm": (_int, [_vp, _vp, _vp, _int, _int, _int]),
+    "fdl_add_row_bias": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "fdl_relu": (_int, [_vp, _vp, _i64, _vp]),
+    "fdl_relu_backward": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "fdl_colsum": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "fdl_softmax": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "fdl_softmax_xent": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "fdl_sgd_update": (_int, [_vp, _vp, _flt, _i64, _vp]),
+    "fdl_mlp2_train_step": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _flt,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fdl_fill_uniform": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
+    "fdl_fill_normal": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
+    "fdl_last_error": (ctypes.c_char_p, []),
+    "fdl_status_string": (ctypes.c_char_p, [_int]),
+    "fdl_version": (ctypes.c_char_p, []),
+}
+
+
+class FdlError(RuntimeError):
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed with status {status}: {message}")
+        self.status = status
+
+
+def library_path() -> str:
+    return os.path.join(_PKG, "libfastdl_gemm.so")
+
+
+def load_library() -> ctypes.CDLL:
+    """Load ``libfastdl_gemm.so``; raise if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _checked(name: str):
+    def call(*args):
+        lib = load_library()
+        status = getattr(lib, name)(*args)
+        if status != 0:
+            raise FdlError(name, status, lib.fdl_last_error().decode())
+        return status
+    call.__name__ = name
+    return call
+
+
+sgemm_ex = _checked("fdl_sgemm_ex")
+sgemm_ex_select = _checked("fdl_sgemm_ex_select")
+gemm = _checked("fdl_gemm")
+add_row_bias = _checked("fdl_add_row_bias")
+relu = _checked("fdl_relu")
+relu_backward = _checked("fdl_relu_backward")
+colsum = _checked("fdl_colsum")
+softmax = _checked("fdl_softmax")
+softmax_xent = _checked("fdl_softmax_xent")
+sgd_update = _checked("fdl_sgd_update")
+mlp2_train_step = _checked("fdl_mlp2_train_step")
+fill_uniform = _checked("fdl_fill_uniform")
+fill_normal = _checked("fdl_fill_normal")
+
+
+def kernel_choice(transA: int, transB: int, M: int, N: int, K: int, batch: int = 1) -> int:
+    return load_library().fdl_sgemm_kernel_choice(transA, transB, M, N, K, batch)
+
+
+def version() -> str:
+    return load_library().fdl_version().decode()
+
+
+def raw_call(name: str, *args) -> int:
+    """Call an entry point and return its status without raising (for error-path tests)."""
+    return getattr(load_library(), name)(*args)
+
+
+def last_error() -> str:
+    return load_library().fdl_last_error().decode()

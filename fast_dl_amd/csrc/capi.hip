@@ -1,0 +1,284 @@
+// extern "C" entry points declared in include/fastdl_gemm.h: argument
+// validation, status codes and dispatch onto the kernels.  Nothing here
+// allocates memory or synchronises the stream.
+#include "fdl_internal.hpp"
+
+#include "../../include/fastdl_gemm.h"
+
+#include <climits>
+#include <cstdio>
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& msg) {
+    g_last_error = msg;
+    return status;
+}
+
+int check_hip(hipError_t err, const char* what) {
+    if (err == hipSuccess) return FDL_SUCCESS;
+    return fail(FDL_ERROR_LAUNCH, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                        const float* A, int64_t lda, int64_t strideA, const float* B,
+                        int64_t ldb, int64_t strideB, float* C, int64_t ldc,
+                        int64_t strideC, int64_t batch, const float* bias,
+                        const float* aux, int epilogue, int kernel, void* stream) {
+    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_SKINNY) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
+    }
+    if ((transA != FDL_OP_N && transA != FDL_OP_T) ||
+        (transB != FDL_OP_N && transB != FDL_OP_T)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: transA/transB must be FDL_OP_N or FDL_OP_T");
+    }
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: M, N, K must be in [0, INT_MAX]");
+    }
+    if (batch < 0) return fail(FDL_ERROR_INVALID_VALUE, "sgemm: batch must be >= 0");
+    if (epilogue < FDL_EPILOGUE_NONE || epilogue > FDL_EPILOGUE_RELU_GRAD) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown epilogue");
+    }
+    const bool ta = transA == FDL_OP_T;
+    const bool tb = transB == FDL_OP_T;
+    const int64_t a_cols = ta ? M : K;
+    const int64_t b_cols = tb ? K : N;
+    if (lda < std::max<int64_t>(1, a_cols)) return fail(FDL_ERROR_INVALID_VALUE, "sgemm: lda too small");
+    if (ldb < std::max<int64_t>(1, b_cols)) return fail(FDL_ERROR_INVALID_VALUE, "sgemm: ldb too small");
+    if (ldc < std::max<int64_t>(1, N)) return fail(FDL_ERROR_INVALID_VALUE, "sgemm: ldc too small");
+    if (strideA < 0 || strideB < 0 || strideC < 0) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: strides must be >= 0");
+    }
+    if (batch == 0 || M == 0 || N == 0) return FDL_SUCCESS;
+    if (batch > 1 && strideC < (M - 1) * ldc + N) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: strideC makes output batches overlap");
+    }
+    if (C == nullptr) return fail(FDL_ERROR_INVALID_VALUE, "sgemm: C is null");
+    if (K > 0 && (A == nullptr || B == nullptr)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: A or B is null");
+    }
+    if ((epilogue == FDL_EPILOGUE_BIAS || epilogue == FDL_EPILOGUE_BIAS_RELU) && bias == nullptr) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: bias epilogue needs a bias pointer");
+    }
+    if (epilogue == FDL_EPILOGUE_RELU_GRAD && aux == nullptr) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: RELU_GRAD epilogue needs an aux pointer");
+    }
+
+    fdl::GemmParams p{};
+    p.A = A;
+    p.B = B;
+    p.C = C;
+    p.bias = bias;
+    p.aux = (epilogue == FDL_EPILOGUE_RELU_GRAD) ? aux : nullptr;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.ldc = ldc;
+    p.strideA = strideA;
+    p.strideB = strideB;
+    p.strideC = strideC;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.epilogue = epilogue;
+    const fdl::GemmKernel kern = static_cast<fdl::GemmKernel>(kernel);
+    if (kern == fdl::GemmKernel::Skinny && (tb || M > 8)) {
+        return fail(FDL_ERROR_NOT_SUPPORTED, "sgemm: skinny kernel needs M <= 8 and B not transposed");
+    }
+    return check_hip(fdl::launch_sgemm(p, ta, tb, batch, kern, as_stream(stream)),
+                     "sgemm launch failed");
+}
+
+int fdl_sgemm_ex(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                 const float* A, int64_t lda, int64_t strideA, const float* B,
+                 int64_t ldb, int64_t strideB, float* C, int64_t ldc,
+                 int64_t strideC, int64_t batch, const float* bias,
+                 const float* aux, int epilogue, void* stream) {
+    return fdl_sgemm_ex_select(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB,
+                               C, ldc, strideC, batch, bias, aux, epilogue,
+                               FDL_KERNEL_AUTO, stream);
+}
+
+int fdl_sgemm_kernel_choice(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                            int64_t batch) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K) || batch < 1) return FDL_KERNEL_AUTO;
+    fdl::GemmParams p{};
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    return static_cast<int>(fdl::choose_kernel(p, transA == FDL_OP_T, transB == FDL_OP_T, batch));
+}
+
+int fdl_gemm(const float* a, const float* b, float* c, int m, int n, int k) {
+    if (m < 0 || n < 0 || k < 0) return fail(FDL_ERROR_INVALID_VALUE, "gemm: negative size");
+    return fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, m, n, k, a, std::max(k, 1), 0, b,
+                        std::max(n, 1), 0, c, std::max(n, 1), 0, 1, nullptr, nullptr,
+                        FDL_EPILOGUE_NONE, nullptr);
+}
+
+int fdl_add_row_bias(float* out, const float* bias, int64_t rows, int64_t cols,
+                     void* stream) {
+    if (rows < 0 || cols < 0) return fail(FDL_ERROR_INVALID_VALUE, "add_row_bias: negative size");
+    if (rows * cols == 0) return FDL_SUCCESS;
+    if (!out || !bias) return fail(FDL_ERROR_INVALID_VALUE, "add_row_bias: null pointer");
+    return check_hip(fdl::launch_add_row_bias(out, bias, rows, cols, as_stream(stream)),
+                     "add_row_bias launch failed");
+}
+
+int fdl_relu(const float* in, float* out, int64_t n, void* stream) {
+    if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "relu: negative size");
+    if (n == 0) return FDL_SUCCESS;
+    if (!in || !out) return fail(FDL_ERROR_INVALID_VALUE, "relu: null pointer");
+    return check_hip(fdl::launch_relu(in, out, n, as_stream(stream)), "relu launch failed");
+}
+
+int fdl_relu_backward(const float* grad_out, const float* act, float* grad_in,
+                      int64_t n, void* stream) {
+    if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "relu_backward: negative size");
+    if (n == 0) return FDL_SUCCESS;
+    if (!grad_out || !act || !grad_in) {
+        return fail(FDL_ERROR_INVALID_VALUE, "relu_backward: null pointer");
+    }
+    return check_hip(fdl::launch_relu_backward(grad_out, act, grad_in, n, as_stream(stream)),
+                     "relu_backward launch failed");
+}
+
+int fdl_colsum(const float* x, float* out, int64_t rows, int64_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return fail(FDL_ERROR_INVALID_VALUE, "colsum: negative size");
+    if (cols == 0) return FDL_SUCCESS;
+    if (!out || (rows > 0 && !x)) return fail(FDL_ERROR_INVALID_VALUE, "colsum: null pointer");
+    return check_hip(fdl::launch_colsum(x, out, rows, cols, as_stream(stream)),
+                     "colsum launch failed");
+}
+
+int fdl_softmax(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
+    if (rows <= 0 || cols <= 0) {
+        return fail(FDL_ERROR_INVALID_VALUE, "softmax: rows and cols must be non-zero");
+    }
+    if (!in || !out) return fail(FDL_ERROR_INVALID_VALUE, "softmax: null pointer");
+    return check_hip(fdl::launch_softmax(in, out, rows, cols, as_stream(stream)),
+                     "softmax launch failed");
+}
+
+int fdl_softmax_xent(const float* logits, const int64_t* labels, float* loss,
+                     float* grad, int64_t batch, int64_t classes, void* stream) {
+    if (batch <= 0) return fail(FDL_ERROR_INVALID_VALUE, "softmax_xent: batch must be positive");
+    if (classes <= 0) {
+        return fail(FDL_ERROR_INVALID_VALUE, "softmax_xent: class count must be positive");
+    }
+    if (!logits || !labels || (!loss && !grad)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "softmax_xent: null pointer");
+    }
+    return check_hip(fdl::launch_softmax_xent(logits, labels, loss, grad, batch, classes,
+                                              as_stream(stream)),
+                     "softmax_xent launch failed");
+}
+
+int fdl_sgd_update(float* param, const float* grad, float lr, int64_t n, void* stream) {
+    if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "sgd_update: negative size");
+    if (n == 0) return FDL_SUCCESS;
+    if (!param || !grad) return fail(FDL_ERROR_INVALID_VALUE, "sgd_update: null pointer");
+    return check_hip(fdl::launch_sgd(param, grad, lr, n, as_stream(stream)),
+                     "sgd_update launch failed");
+}
+
+int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
+                        int64_t in_features, int64_t hidden, int64_t classes,
+                        float* W1, float* b1, float* W2, float* b2, float lr,
+                        float* H, float* logits, float* G2, float* G1, float* dW1,
+                        float* db1, float* dW2, float* db2, float* dX, float* loss,
+                        void* stream) {
+    if (batch <= 0 || in_features <= 0 || hidden <= 0 || classes <= 0 ||
+        !fits_int(batch) || !fits_int(in_features) || !fits_int(hidden) ||
+        !fits_int(classes)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "mlp2_train_step: sizes must be positive ints");
+    }
+    if (!X || !labels || !W1 || !b1 || !W2 || !b2 || !H || !logits || !G2 || !G1 ||
+        !dW1 || !db1 || !dW2 || !db2 || !loss) {
+        return fail(FDL_ERROR_INVALID_VALUE, "mlp2_train_step: null pointer");
+    }
+    const int64_t B = batch, I = in_features, Hd = hidden, Cc = classes;
+    int st;
+    // Forward: H = relu(X W1 + b1), logits = H W2 + b2.
+    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Hd, I, X, I, 0, W1, Hd, 0, H, Hd, 0, 1, b1,
+                      nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
+    if (st) return st;
+    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Cc, Hd, H, Hd, 0, W2, Cc, 0, logits, Cc, 0, 1,
+                      b2, nullptr, FDL_EPILOGUE_BIAS, stream);
+    if (st) return st;
+    // Loss and dL/dlogits.
+    st = fdl_softmax_xent(logits, labels, loss, G2, B, Cc, stream);
+    if (st) return st;
+    // Layer 2 backward: dW2 = H^T G2 (TN), db2 = colsum(G2),
+    // G1 = (G2 W2^T) masked by H > 0 (NT with the ReLU-gradient epilogue).
+    st = fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, Hd, Cc, B, H, Hd, 0, G2, Cc, 0, dW2, Cc, 0, 1,
+                      nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
+    if (st) return st;
+    st = fdl_colsum(G2, db2, B, Cc, stream);
+    if (st) return st;
+    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, Hd, Cc, G2, Cc, 0, W2, Cc, 0, G1, Hd, 0, 1,
+                      nullptr, H, FDL_EPILOGUE_RELU_GRAD, stream);
+    if (st) return st;
+    // Layer 1 backward: dW1 = X^T G1 (TN), db1 = colsum(G1), dX = G1 W1^T (NT).
+    st = fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, I, Hd, B, X, I, 0, G1, Hd, 0, dW1, Hd, 0, 1,
+                      nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
+    if (st) return st;
+    st = fdl_colsum(G1, db1, B, Hd, stream);
+    if (st) return st;
+    if (dX) {
+        st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, I, Hd, G1, Hd, 0, W1, Hd, 0, dX, I, 0, 1,
+                          nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
+        if (st) return st;
+    }
+    // SGD on all four parameters in one launch.
+    float* params[4] = {W1, b1, W2, b2};
+    const float* grads[4] = {dW1, db1, dW2, db2};
+    const int64_t sizes[4] = {I * Hd, Hd, Hd * Cc, Cc};
+    return check_hip(fdl::launch_sgd_multi(4, params, grads, sizes, lr, as_stream(stream)),
+                     "mlp2_train_step sgd launch failed");
+}
+
+int fdl_fill_uniform(float* data, int64_t n, float low, float high, uint64_t seed,
+                     void* stream) {
+    if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "fill_uniform: negative size");
+    if (n == 0) return FDL_SUCCESS;
+    if (!data) return fail(FDL_ERROR_INVALID_VALUE, "fill_uniform: null pointer");
+    return check_hip(fdl::launch_fill_uniform(data, n, low, high, seed, as_stream(stream)),
+                     "fill_uniform launch failed");
+}
+
+int fdl_fill_normal(float* data, int64_t n, float mean, float stddev, uint64_t seed,
+                    void* stream) {
+    if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "fill_normal: negative size");
+    if (n == 0) return FDL_SUCCESS;
+    if (!data) return fail(FDL_ERROR_INVALID_VALUE, "fill_normal: null pointer");
+    return check_hip(fdl::launch_fill_normal(data, n, mean, stddev, seed, as_stream(stream)),
+                     "fill_normal launch failed");
+}
+
+const char* fdl_last_error(void) { return g_last_error.c_str(); }
+
+const char* fdl_status_string(int status) {
+    switch (status) {
+        case FDL_SUCCESS: return "FDL_SUCCESS";
+        case FDL_ERROR_INVALID_VALUE: return "FDL_ERROR_INVALID_VALUE";
+        case FDL_ERROR_NOT_SUPPORTED: return "FDL_ERROR_NOT_SUPPORTED";
+        case FDL_ERROR_LAUNCH: return "FDL_ERROR_LAUNCH";
+        case FDL_ERROR_RUNTIME: return "FDL_ERROR_RUNTIME";
+    }
+    return "FDL_UNKNOWN_STATUS";
+}
+
+const char* fdl_version(void) { return "fastdl_gemm 0.1.0 gfx950"; }
+
+}  // extern "C"

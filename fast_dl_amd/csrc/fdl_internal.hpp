@@ -1,0 +1,79 @@
+// Internal declarations shared by the HIP translation units of libfastdl_gemm.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fdl {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+enum Epilogue : int {
+    EPI_NONE = 0,
+    EPI_BIAS = 1,
+    EPI_BIAS_RELU = 2,
+    EPI_RELU = 3,
+    EPI_RELU_GRAD = 4,
+};
+
+// One strided-batched GEMM problem, already validated on the host.
+// Sizes fit in int32 (the reference's own API is int-sized); offsets are int64.
+struct GemmParams {
+    const float* A;
+    const float* B;
+    float* C;
+    const float* bias;  // length N, or null
+    const float* aux;   // same layout as C (ldc, strideC), or null
+    int64_t lda, ldb, ldc;
+    int64_t strideA, strideB, strideC;
+    int M, N, K;
+    int epilogue;
+};
+
+// Kernel families; the host dispatcher picks one per call.
+enum class GemmKernel : int {
+    Tiled128 = 0,   // 128x128x16 LDS double-buffered MFMA tile
+    Tiled64 = 1,    // 64x64x16 LDS double-buffered MFMA tile
+    SplitK32 = 2,   // 32x32 output tile, K split over the waves of a block
+    Skinny = 3,     // VALU strip kernel for M <= 8 with B not transposed
+    Auto = -1,
+};
+
+// Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
+hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,
+                        int64_t batch, GemmKernel kernel, hipStream_t stream);
+
+// Kernel the dispatcher would pick for this problem.
+GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
+                         int64_t batch);
+
+const char* kernel_name(GemmKernel k);
+
+// Elementwise / row kernels (mlp_kernels.hip).
+hipError_t launch_add_row_bias(float* out, const float* bias, int64_t rows,
+                               int64_t cols, hipStream_t stream);
+hipError_t launch_relu(const float* in, float* out, int64_t n,
+                       hipStream_t stream);
+hipError_t launch_relu_backward(const float* g, const float* act, float* out,
+                                int64_t n, hipStream_t stream);
+hipError_t launch_colsum(const float* x, float* out, int64_t rows, int64_t cols,
+                         hipStream_t stream);
+hipError_t launch_softmax(const float* in, float* out, int64_t rows,
+                          int64_t cols, hipStream_t stream);
+hipError_t launch_softmax_xent(const float* logits, const int64_t* labels,
+                               float* loss, float* grad, int64_t batch,
+                               int64_t classes, hipStream_t stream);
+hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,
+                      hipStream_t stream);
+// Up to four (param, grad, n) updates in one launch.
+hipError_t launch_sgd_multi(int count, float* const* params,
+                            const float* const* grads, const int64_t* sizes,
+                            float lr, hipStream_t stream);
+hipError_t launch_fill_uniform(float* data, int64_t n, float low, float high,
+                               uint64_t seed, hipStream_t stream);
+hipError_t launch_fill_normal(float* data, int64_t n, float mean, float stddev,
+                              uint64_t seed, hipStream_t stream);
+
+}  // namespace fdl

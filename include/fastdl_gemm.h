@@ -1,0 +1,233 @@
+/*
+ * fastdl_gemm.h -- C-ABI of the MI355X (gfx950) fp32 GEMM path.
+ *
+ * Plain C: pointers, sizes and status codes only.  Every pointer argument that
+ * names a matrix or vector is a device pointer (HBM) on the calling thread's
+ * current HIP device.  `stream` is a hipStream_t passed as void*; NULL means
+ * the device's null stream, which is what the reference's implicit
+ * legacy-default-stream launches used.
+ *
+ * No entry point allocates device or host memory, none throws, and all are
+ * asynchronous with respect to the host: they only validate arguments and
+ * enqueue kernels.  A non-zero return is one of the negative fdl_status
+ * codes; fdl_last_error() returns a message for the last failure on the
+ * calling thread.
+ *
+ * Layout convention: row-major everywhere, as in the reference.  For the
+ * general entry point, with op(X) = X or X^T:
+ *
+ *   C[b][i][j] = epi( sum_k op(A)[b][i][k] * op(B)[b][k][j] ,  i, j )
+ *
+ *   op(A)[i][k] = A[i*lda + k]  (transA == FDL_OP_N)  A holds M x K
+ *               = A[k*lda + i]  (transA == FDL_OP_T)  A holds K x M
+ *   op(B)[k][j] = B[k*ldb + j]  (transB == FDL_OP_N)  B holds K x N
+ *               = B[j*ldb + k]  (transB == FDL_OP_T)  B holds N x K
+ *
+ * C is overwritten (beta = 0), as cublasSgemm was called with beta = 0 in
+ * the reference (src/kernels/cuda/gemm.cu:172-175).
+ */
+#ifndef FASTDL_GEMM_H
+#define FASTDL_GEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fdl_status {
+    FDL_SUCCESS = 0,
+    FDL_ERROR_INVALID_VALUE = -1,   /* bad size, leading dimension, pointer or enum */
+    FDL_ERROR_NOT_SUPPORTED = -2,   /* valid request this build does not implement */
+    FDL_ERROR_LAUNCH = -3,          /* kernel launch failed (hipGetLastError) */
+    FDL_ERROR_RUNTIME = -4          /* other HIP runtime failure */
+} fdl_status;
+
+typedef enum fdl_operation {
+    FDL_OP_N = 0,
+    FDL_OP_T = 1
+} fdl_operation;
+
+/* Epilogue applied to each accumulated element v = sum_k(...) at (i, j). */
+typedef enum fdl_epilogue {
+    FDL_EPILOGUE_NONE = 0,       /* C = v                                      */
+    FDL_EPILOGUE_BIAS = 1,       /* C = v + bias[j]                            */
+    FDL_EPILOGUE_BIAS_RELU = 2,  /* C = fmaxf(0, v + bias[j])                  */
+    FDL_EPILOGUE_RELU = 3,       /* C = fmaxf(0, v)                            */
+    FDL_EPILOGUE_RELU_GRAD = 4   /* C = aux[i][j] > 0 ? v : 0  (ReLU backward; */
+                                 /*     aux has C's ldc and strideC)           */
+} fdl_epilogue;
+
+/*
+ * General strided-batched fp32 GEMM with optional fused epilogue.
+ *
+ * Replaces cublasSgemm in launch_gemm_cublas (src/kernels/cuda/gemm.cu:166-177)
+ * and the separate add_row_bias pass that ops::linear runs after it
+ * (src/ops/Linear.cpp:38-44, src/kernels/cuda/bias.cu:5-12).  Transposed
+ * operands serve the NT / TN products of linear backward
+ * (legacy/src/ops/Layers.cpp:36,40).
+ *
+ * M, N, K >= 0; batch >= 0 (0 or an empty C is a no-op, K == 0 gives
+ * C = epi(0)).  lda >= max(1, columns of A as stored), same for ldb, ldc.
+ * Strides are in elements and may be 0 (broadcast), except strideC which
+ * must be >= M*ldc when batch > 1 so that batches do not overlap.
+ * bias (length N, shared by every batch) is required for the BIAS epilogues;
+ * aux is required for RELU_GRAD.
+ */
+int fdl_sgemm_ex(int transA, int transB,
+                 int64_t M, int64_t N, int64_t K,
+                 const float* A, int64_t lda, int64_t strideA,
+                 const float* B, int64_t ldb, int64_t strideB,
+                 float* C, int64_t ldc, int64_t strideC,
+                 int64_t batch,
+                 const float* bias, const float* aux, int epilogue,
+                 void* stream);
+
+/* Kernel families behind fdl_sgemm_ex (what GemmAlgo selected in the
+ * reference, include/dl/kernels/gemm.hpp:7-12; the set is this build's own). */
+typedef enum fdl_kernel {
+    FDL_KERNEL_AUTO = -1,      /* size heuristic (what fdl_sgemm_ex uses)       */
+    FDL_KERNEL_TILED128 = 0,   /* 128x128x16 LDS double-buffered MFMA tile      */
+    FDL_KERNEL_TILED64 = 1,    /* 64x64x16 LDS double-buffered MFMA tile        */
+    FDL_KERNEL_SPLITK32 = 2,   /* 32x32 MFMA tile, K split over 8 waves          */
+    FDL_KERNEL_SKINNY = 3      /* VALU strip kernel, M <= 8 and transB == N     */
+} fdl_kernel;
+
+/*
+ * fdl_sgemm_ex with the kernel family forced, for tests and benchmarks that
+ * must cover every family on the same shape (the reference benchmark ran all
+ * of its GemmAlgo variants the same way, tests/benchmarks/gemm/
+ * gemm_benchmark.cu:86-100).  FDL_KERNEL_SKINNY with M > 8 or transB == T
+ * returns FDL_ERROR_NOT_SUPPORTED.
+ */
+int fdl_sgemm_ex_select(int transA, int transB,
+                        int64_t M, int64_t N, int64_t K,
+                        const float* A, int64_t lda, int64_t strideA,
+                        const float* B, int64_t ldb, int64_t strideB,
+                        float* C, int64_t ldc, int64_t strideC,
+                        int64_t batch,
+                        const float* bias, const float* aux, int epilogue,
+                        int kernel, void* stream);
+
+/* Kernel family fdl_sgemm_ex would use for this problem (FDL_KERNEL_*). */
+int fdl_sgemm_kernel_choice(int transA, int transB,
+                            int64_t M, int64_t N, int64_t K, int64_t batch);
+
+/*
+ * C[m,n] = A[m,k] . B[k,n], row-major, contiguous, null stream.
+ * Same contract as dl::kernels::gemm (include/dl/kernels/gemm.hpp:16-17,
+ * src/kernels/cuda/gemm.cu:197-213) with the algorithm choice internal.
+ */
+int fdl_gemm(const float* a, const float* b, float* c, int m, int n, int k);
+
+/*
+ * out[r, c] += bias[c] in place over a rows x cols row-major matrix.
+ * Replaces dl::kernels::add_row_bias (include/dl/kernels/bias.hpp:5,
+ * src/kernels/cuda/bias.cu:5-28).
+ */
+int fdl_add_row_bias(float* out, const float* bias, int64_t rows, int64_t cols,
+                     void* stream);
+
+/*
+ * out[i] = fmaxf(0, in[i]).  Replaces the ReLU branch of
+ * dl::kernels::activation (src/kernels/cuda/activation.cu:6-17,74-78).
+ */
+int fdl_relu(const float* in, float* out, int64_t n, void* stream);
+
+/*
+ * grad_in[i] = act[i] > 0 ? grad_out[i] : 0, where act is the ReLU input or
+ * output (both are > 0 at the same places).  No reference counterpart exists
+ * (the reference has no ReLU backward); the rule follows the derivative with
+ * the value at exactly 0 taken as 0.
+ */
+int fdl_relu_backward(const float* grad_out, const float* act, float* grad_in,
+                      int64_t n, void* stream);
+
+/*
+ * out[c] = sum_r x[r, c] (rows summed in increasing r order).  The db term of
+ * linear backward, legacy/src/ops/Layers.cpp:44.
+ */
+int fdl_colsum(const float* x, float* out, int64_t rows, int64_t cols,
+               void* stream);
+
+/*
+ * Row softmax, out[r, :] = exp(x - max) / sum(exp(x - max)).
+ * Replaces dl::kernels::softmax as called by ops::softmax
+ * (src/ops/Softmax.cpp:33-38, src/kernels/cuda/softmax.cu:131-254).
+ */
+int fdl_softmax(const float* in, float* out, int64_t rows, int64_t cols,
+                void* stream);
+
+/*
+ * Mean softmax cross-entropy over a batch, and optionally its gradient.
+ *   loss[0] = (1/batch) * sum over rows with 0 <= label < classes of
+ *             (log(sum_c exp(z_c - max)) + max - z_label)
+ *   grad[r, c] = (softmax(z_r)_c - [c == label_r]) / batch   (if grad != NULL)
+ * loss follows dl::kernels::cross_entropy (src/kernels/cuda/cross_entropy.cu:
+ * 9-35): rows with an invalid label add nothing but still count in batch.
+ * grad follows legacy SoftmaxCrossEntropyLoss::backward
+ * (legacy/src/ops/SoftmaxCrossEntropyLoss.cpp:39-51).  loss is written, not
+ * accumulated, so it needs no prior zeroing.
+ */
+int fdl_softmax_xent(const float* logits, const int64_t* labels,
+                     float* loss, float* grad, int64_t batch, int64_t classes,
+                     void* stream);
+
+/*
+ * param[i] -= lr * grad[i].  SGD::step, legacy/include/dl/optim/Optimizer.hpp:
+ * 24-34.
+ */
+int fdl_sgd_update(float* param, const float* grad, float lr, int64_t n,
+                   void* stream);
+
+/*
+ * One training step of the two-layer MLP  in -> hidden (ReLU) -> classes with
+ * softmax cross-entropy and SGD, weights in the active API's [in, out] layout
+ * (src/nn/Linear.cpp:27).  Step order follows legacy Network
+ * (legacy/src/runtime/Network.cpp:7-34): forward, loss, backward through every
+ * layer (dX of the first layer included when dX != NULL), then the update.
+ *
+ *   H      = relu(X W1 + b1)              [batch, hidden]
+ *   logits = H W2 + b2                    [batch, classes]
+ *   G2     = (softmax(logits) - onehot)/batch, loss as fdl_softmax_xent
+ *   dW2 = H^T G2, db2 = colsum(G2), G1 = (G2 W2^T) * [H > 0]
+ *   dW1 = X^T G1, db1 = colsum(G1), dX = G1 W1^T
+ *   W -= lr dW, b -= lr db for both layers
+ *
+ * Every buffer belongs to the caller; the step allocates nothing.  H, logits,
+ * G2, G1, dW1, db1, dW2, db2 hold the step's intermediates on return.
+ */
+int fdl_mlp2_train_step(const float* X, const int64_t* labels,
+                        int64_t batch, int64_t in_features,
+                        int64_t hidden, int64_t classes,
+                        float* W1, float* b1, float* W2, float* b2, float lr,
+                        float* H, float* logits, float* G2, float* G1,
+                        float* dW1, float* db1, float* dW2, float* db2,
+                        float* dX, float* loss, void* stream);
+
+/*
+ * Fill with uniform values in (low, high] or normal values, from a
+ * counter-based Philox4x32-10 stream keyed by seed (element i uses counter i).
+ * Replaces the cuRAND fills of dl::kernels::uniform_float32 / normal_float32
+ * (src/kernels/cuda/random.cu:7-54); the values are NOT bit-identical to
+ * cuRAND's, only the distribution and same-seed determinism match.
+ */
+int fdl_fill_uniform(float* data, int64_t n, float low, float high,
+                     uint64_t seed, void* stream);
+int fdl_fill_normal(float* data, int64_t n, float mean, float stddev,
+                    uint64_t seed, void* stream);
+
+/* Message for the last non-zero status returned on the calling thread. */
+const char* fdl_last_error(void);
+
+/* Name of a status code. */
+const char* fdl_status_string(int status);
+
+/* Build identification string (target architecture and version). */
+const char* fdl_version(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FASTDL_GEMM_H */

@@ -1,0 +1,105 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every symbol the
+public header declares, and rejects invalid arguments before touching a GPU
+(validation never calls into the HIP runtime)."""
+import os
+import re
+
+import numpy as np
+
+import fast_dl_amd.capi as capi
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fastdl_gemm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fdl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = capi.load_library()
+    names = declared_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in fastdl_gemm.h but not exported"
+        assert name in capi.SIGNATURES, f"{name} missing from the ctypes binding"
+    assert "gfx950" in capi.version()
+
+
+def test_status_strings():
+    lib = capi.load_library()
+    assert lib.fdl_status_string(0) == b"FDL_SUCCESS"
+    assert lib.fdl_status_string(-1) == b"FDL_ERROR_INVALID_VALUE"
+
+
+def _sgemm_status(**kw):
+    args = dict(ta=0, tb=0, M=4, N=4, K=4, A=1 << 20, lda=4, sA=0, B=1 << 20, ldb=4, sB=0,
+                C=1 << 20, ldc=4, sC=0, batch=1, bias=None, aux=None, epi=0, stream=None)
+    args.update(kw)
+    return capi.raw_call("fdl_sgemm_ex", *args.values())
+
+
+def test_sgemm_argument_validation():
+    bad = [
+        dict(ta=2), dict(tb=-1), dict(M=-1), dict(K=1 << 31), dict(batch=-1), dict(epi=7),
+        dict(lda=3), dict(ldb=3), dict(ldc=3), dict(ta=1, lda=3), dict(tb=1, ldb=3),
+        dict(sA=-4), dict(batch=2, sC=4), dict(C=None), dict(A=None), dict(B=None),
+        dict(epi=1), dict(epi=2), dict(epi=4),
+    ]
+    for kw in bad:
+        assert _sgemm_status(**kw) == -1, kw
+        assert capi.last_error().startswith("sgemm:")
+
+
+def test_noop_sizes_need_no_gpu():
+    # M == 0, N == 0 or batch == 0: valid and nothing is launched
+    assert _sgemm_status(M=0, A=None, B=None, C=None) == 0
+    assert _sgemm_status(N=0, lda=4, ldb=1, ldc=1, A=None, B=None, C=None) == 0
+    assert _sgemm_status(batch=0, A=None, B=None, C=None) == 0
+
+
+def test_other_entry_points_validate():
+    assert capi.raw_call("fdl_gemm", None, None, None, -1, 2, 2) == -1
+    assert capi.raw_call("fdl_relu", None, None, 5, None) == -1
+    assert capi.raw_call("fdl_relu", None, None, 0, None) == 0
+    assert capi.raw_call("fdl_colsum", None, None, 3, 3, None) == -1
+    assert capi.raw_call("fdl_softmax", 1, 1, 0, 3, None) == -1
+    assert capi.raw_call("fdl_softmax_xent", 1, 1, 1, 1, 4, 0, None) == -1
+    assert "class count" in capi.last_error()
+    assert capi.raw_call("fdl_sgd_update", None, None, 0.1, -1, None) == -1
+    assert capi.raw_call("fdl_sgemm_ex_select", 0, 1, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
+                         1, None, None, 0, 3, None) == -2  # skinny with B transposed
+    assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
+                         1, None, None, 0, 9, None) == -1
+    assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
+                         *([None] * 11)) == -1
+
+
+def test_kernel_choice():
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED128
+    assert capi.kernel_choice(0, 0, 8, 4096, 4096) == capi.KERNEL_SKINNY
+    assert capi.kernel_choice(0, 1, 8, 4096, 4096) != capi.KERNEL_SKINNY
+    assert capi.kernel_choice(0, 0, 256, 128, 784) == capi.KERNEL_SPLITK32
+
+
+def test_golden_fixtures_reproduced_by_oracle():
+    import hashlib
+
+    gold = np.load(os.path.join(ROOT, "tests", "golden", "config1_gemm.npz"))
+    g = np.random.default_rng(1)
+    A = g.random((1, 256, 784)).astype(np.float32)
+    B = (g.standard_normal((1, 784, 128)) * np.sqrt(2.0 / 784)).astype(np.float32)
+    assert hashlib.sha256(A.tobytes()).digest() == gold["sha_A"].tobytes()
+    assert hashlib.sha256(B.tobytes()).digest() == gold["sha_B"].tobytes()
+    assert np.array_equal(oracle.gemm_cpu(A[0], B[0]), gold["C32"])
+    c64 = A[0].astype(np.float64) @ B[0].astype(np.float64)
+    assert np.allclose(gold["C64"], c64, rtol=1e-12, atol=1e-12)
+
+    m = np.load(os.path.join(ROOT, "tests", "golden", "mlp2_small_step.npz"))
+    out = oracle.mlp2_train_step(m["X"], m["labels"], m["W1"], m["b1"], m["W2"], m["b2"],
+                                 float(m["lr"]))
+    for k in ("W1", "b1", "W2", "b2", "dX", "loss"):
+        assert np.array_equal(out[k], m[f"out_{k}"]), k
