@@ -40,6 +40,9 @@ def parse_args():
     ap.add_argument("--sweep", default=None, help="write every BASELINE config's timing here")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the headline launches (for rocprofv3 runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="with --profile-mode: also run a 256 MiB device copy, the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -223,6 +226,12 @@ def main():
     stream = torch.cuda.current_stream()
     ms = time_launches(launch, args.steps, args.warmup, stream)
     if args.profile_mode:
+        if args.copy_calib:
+            src = torch.ones(64 << 20, device="cuda")  # 256 MiB
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
         print(json.dumps({"profile_mode": True, "ms_per_launch": ms}), flush=True)
         return
     flops = 2.0 * n * n * n

@@ -54,11 +54,18 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+# Host-only C++ (the dl:: API) is plain C++17 against the HIP runtime API.
+HOST_CXX = os.environ.get("CXX_HOST", "g++")
+HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+              "-I", INCLUDE, "-I", os.path.join(ROCM, "include")]
+
+
 def _compile(src: str, obj: str, device: bool) -> str:
-    cmd = [HIPCC, *COMMON_FLAGS]
     if device:
-        cmd += DEVICE_FLAGS
-    cmd += ["-c", src, "-o", obj]
+        cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HOST_CXX, *HOST_FLAGS, "-c", src, "-o", obj]
     _run(cmd)
     return obj
 
@@ -92,8 +99,9 @@ def build_dl_library() -> str | None:
         list(ex.map(lambda so: _compile(so[0], so[1], False), zip(srcs, objs)))
     out = os.path.join(PKG, "libfastdl.so")
     tmp = out + ".tmp"
-    _run([HIPCC, "-shared", "-fPIC", "-o", tmp, *objs,
-          "-L", PKG, "-lfastdl_gemm", "-Wl,-rpath,$ORIGIN"])
+    _run([HOST_CXX, "-shared", "-fPIC", "-o", tmp, *objs,
+          "-L", PKG, "-lfastdl_gemm", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
     os.replace(tmp, out)
     return out
 
@@ -108,8 +116,8 @@ def build_cpp_tests() -> list[str]:
 
     def one(src: str) -> str:
         exe = os.path.join(bindir, os.path.splitext(os.path.basename(src))[0])
-        _run([HIPCC, "-O2", "-std=c++17", "-I", INCLUDE, src, "-o", exe,
-              "-L", PKG, "-lfastdl", "-lfastdl_gemm", f"-Wl,-rpath,{PKG}",
+        _run([HOST_CXX, "-O2", "-std=c++17", "-I", INCLUDE, src, "-o", exe,
+              "-L", PKG, "-lfastdl", "-lfastdl_gemm",
               "-Wl,-rpath,$ORIGIN/../../../fast_dl_amd"])
         return exe
 

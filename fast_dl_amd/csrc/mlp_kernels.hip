@@ -95,8 +95,7 @@ __global__ void softmax_kernel(const float* __restrict__ in, float* __restrict__
     float s = 0.0f;
     for (int64_t c = lane; c < cols; c += 64) s += expf(x[c] - mx);
     s = wave_sum(s);
-    const float inv = 1.0f / s;
-    for (int64_t c = lane; c < cols; c += 64) y[c] = expf(x[c] - mx) * inv;
+    for (int64_t c = lane; c < cols; c += 64) y[c] = expf(x[c] - mx) / s;
 }
 
 // Softmax cross-entropy over the whole batch in one block: thread t owns rows
@@ -137,8 +136,11 @@ softmax_xent_kernel(const float* __restrict__ logits,
     if (threadIdx.x == 0 && loss) loss[0] = part[0];
 }
 
+// p -= lr * g with the product rounded before the subtraction (no FMA
+// contraction), as the reference's x86 host update computes it.
 __global__ void sgd_kernel(float* __restrict__ p, const float* __restrict__ g,
                            float lr, int64_t n) {
+#pragma clang fp contract(off)
     for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
         p[idx] -= lr * g[idx];
@@ -153,6 +155,7 @@ struct SgdMulti {
 
 // blockIdx.y selects the tensor; the x grid strides over the largest one.
 __global__ void sgd_multi_kernel(SgdMulti args, float lr) {
+#pragma clang fp contract(off)
     const int t = blockIdx.y;
     float* __restrict__ p = args.p[t];
     const float* __restrict__ g = args.g[t];

@@ -69,9 +69,8 @@ __device__ __forceinline__ float apply_epilogue(float v, int epi,
 // base is 16-byte aligned, so a float4 is either wholly inside or wholly
 // outside the matrix.
 // ---------------------------------------------------------------------------
-template <int MN, int BK, int NT, bool KCONTIG, bool VEC>
+template <int MN, int BK, int NT, int PAD, bool KCONTIG, bool VEC>
 struct TileLoader {
-    static constexpr int PAD = 4;
     static constexpr int LD = MN + PAD;
     static constexpr int VW = VEC ? 4 : 1;
     static constexpr int SLOTS = MN * BK / (VW * NT);
@@ -137,25 +136,33 @@ struct TileLoader {
 };
 
 // ---------------------------------------------------------------------------
-// LDS double-buffered MFMA tile kernel.  256 threads = 4 waves arranged
-// (BM/WM) x (BN/WN); each wave owns a WM x WN block of C made of
-// (WM/32) x (WN/32) MFMA 32x32 accumulators.  Per K-tile: the next tile's
-// global loads are issued first, the current LDS buffer feeds the MFMAs, then
-// the prefetched registers go to the other LDS buffer and one barrier closes
-// the step.
+// LDS double-buffered MFMA tile kernel.  NT = 64 * (BM/WM) * (BN/WN) threads;
+// each wave owns a WM x WN block of C made of (WM/32) x (WN/32) MFMA 32x32
+// accumulators.  Per K-tile: the next tile's global loads are issued first,
+// the current LDS buffer feeds the MFMAs, then the prefetched registers go to
+// the other LDS buffer and one barrier closes the step.  PAD floats of padding
+// per LDS row; WPE is the minimum number of waves per SIMD the register
+// allocation must allow (occupancy target).
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
-__global__ void __launch_bounds__(256)
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int PAD_, int WPE_, int PRIO_ = 0>
+struct TileCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int PAD = PAD_, WPE = WPE_, PRIO = PRIO_;
+    static constexpr int NT = kWave * (BM / WM) * (BN / WN);
+};
+
+template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(Cfg::NT, Cfg::WPE)
 sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
-    constexpr int NT = 256;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, WM = Cfg::WM, WN = Cfg::WN;
+    constexpr int NT = Cfg::NT;
     constexpr int FM = WM / 32;
     constexpr int FN = WN / 32;
     constexpr int WGM = BM / WM;
-    static_assert((BM / WM) * (BN / WN) == NT / kWave, "4 waves per block");
     static_assert(BK % 2 == 0, "MFMA consumes k in pairs");
 
-    using LoaderA = TileLoader<BM, BK, NT, !TA, VA>;
-    using LoaderB = TileLoader<BN, BK, NT, TB, VB>;
+    using LoaderA = TileLoader<BM, BK, NT, Cfg::PAD, !TA, VA>;
+    using LoaderB = TileLoader<BN, BK, NT, Cfg::PAD, TB, VB>;
     __shared__ __attribute__((aligned(16))) float As[2][BK * LoaderA::LD];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LoaderB::LD];
 
@@ -209,23 +216,31 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
             }
             const float* __restrict__ as = As[cur];
             const float* __restrict__ bs = Bs[cur];
+            // Read every operand fragment of this K-tile before the first MFMA,
+            // so the LDS latency is paid once per tile rather than per k pair.
+            float a[BK / 2][FM];
+            float b[BK / 2][FN];
 #pragma unroll
-            for (int kk = 0; kk < BK; kk += 2) {
-                float a[FM];
-                float b[FN];
+            for (int kp = 0; kp < BK / 2; ++kp) {
 #pragma unroll
                 for (int mi = 0; mi < FM; ++mi)
-                    a[mi] = as[(kk + half) * LoaderA::LD + wm0 + mi * 32 + l32];
+                    a[kp][mi] = as[(2 * kp + half) * LoaderA::LD + wm0 + mi * 32 + l32];
 #pragma unroll
                 for (int ni = 0; ni < FN; ++ni)
-                    b[ni] = bs[(kk + half) * LoaderB::LD + wn0 + ni * 32 + l32];
+                    b[kp][ni] = bs[(2 * kp + half) * LoaderB::LD + wn0 + ni * 32 + l32];
+            }
+            // Keep the scheduler from sinking the reads back next to their MFMAs.
+            __builtin_amdgcn_sched_barrier(0);
+            if (Cfg::PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int kp = 0; kp < BK / 2; ++kp)
 #pragma unroll
                 for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
                     for (int ni = 0; ni < FN; ++ni)
                         acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-            }
+                            a[kp][mi], b[kp][ni], acc[mi][ni], 0, 0, 0);
+            if (Cfg::PRIO) __builtin_amdgcn_s_setprio(0);
             if (has_next) {
                 la.store(As[cur ^ 1], tid);
                 lb.store(Bs[cur ^ 1], tid);
@@ -236,17 +251,27 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 
     float* __restrict__ C = p.C + bz * p.strideC;
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    const int epi = p.epilogue;
+    const bool has_bias = epi == EPI_BIAS || epi == EPI_BIAS_RELU;
+    const bool relu = epi == EPI_BIAS_RELU || epi == EPI_RELU;
 #pragma unroll
-    for (int mi = 0; mi < FM; ++mi) {
+    for (int ni = 0; ni < FN; ++ni) {
+        const int j = n0 + wn0 + ni * 32 + l32;
+        const bool j_ok = j < p.N;
+        // One bias value per lane and column block, loaded once.
+        const float bj = (has_bias && j_ok) ? p.bias[j] : 0.0f;
 #pragma unroll
-        for (int ni = 0; ni < FN; ++ni) {
-            const int j = n0 + wn0 + ni * 32 + l32;
+        for (int mi = 0; mi < FM; ++mi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int i = m0 + wm0 + mi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (i < p.M && j < p.N) {
+                if (j_ok && i < p.M) {
                     const int64_t off = (int64_t)i * p.ldc + j;
-                    C[off] = apply_epilogue(acc[mi][ni][r], p.epilogue, p.bias, aux, off, j);
+                    float v = acc[mi][ni][r];
+                    if (has_bias) v += bj;
+                    if (relu) v = fmaxf(0.0f, v);
+                    if (epi == EPI_RELU_GRAD) v = aux[off] > 0.0f ? v : 0.0f;
+                    C[off] = v;
                 }
             }
         }
@@ -462,19 +487,18 @@ inline bool vec_ok(const float* ptr, int64_t contig_extent, int64_t ld,
            (batch <= 1 || stride % 4 == 0);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <class Cfg>
 hipError_t launch_tiled(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                         int nbatch, hipStream_t stream) {
-    constexpr int BK = 16;
-    const int tiles_m = (p.M + BM - 1) / BM;
-    const int tiles_n = (p.N + BN - 1) / BN;
+    const int tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    const int tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const dim3 grid(tiles_m * tiles_n, nbatch);
-    const dim3 block(256);
+    const dim3 block(Cfg::NT);
     const int code = (ta ? 8 : 0) | (tb ? 4 : 0) | (va ? 2 : 0) | (vb ? 1 : 0);
 #define FDL_TILED_CASE(C, TA_, TB_, VA_, VB_)                                         \
     case C:                                                                           \
-        hipLaunchKernelGGL((sgemm_tiled_kernel<BM, BN, BK, WM, WN, TA_, TB_, VA_, VB_>), \
-                           grid, block, 0, stream, p, tiles_m, tiles_n);              \
+        hipLaunchKernelGGL((sgemm_tiled_kernel<Cfg, TA_, TB_, VA_, VB_>), grid, block, 0, \
+                           stream, p, tiles_m, tiles_n);                            \
         break;
     switch (code) {
         FDL_TILED_CASE(0, false, false, false, false)
@@ -561,6 +585,10 @@ hipError_t launch_skinny(const GemmParams& p, bool ta, bool vb, int nbatch,
 
 constexpr int kMaxGridY = 65535;
 
+// Production tile configurations (BM, BN, BK, WM, WN, PAD, waves per SIMD).
+using CfgTiled128 = TileCfg<128, 128, 16, 64, 64, 4, 1>;
+using CfgTiled64 = TileCfg<64, 64, 16, 32, 32, 4, 1>;
+
 }  // namespace
 
 const char* kernel_name(GemmKernel k) {
@@ -607,10 +635,10 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
         hipError_t err = hipSuccess;
         switch (kernel) {
             case GemmKernel::Tiled128:
-                err = launch_tiled<128, 128, 64, 64>(p, transA, transB, va, vb, nb, stream);
+                err = launch_tiled<CfgTiled128>(p, transA, transB, va, vb, nb, stream);
                 break;
             case GemmKernel::Tiled64:
-                err = launch_tiled<64, 64, 32, 32>(p, transA, transB, va, vb, nb, stream);
+                err = launch_tiled<CfgTiled64>(p, transA, transB, va, vb, nb, stream);
                 break;
             case GemmKernel::SplitK32:
                 err = launch_splitk32(p, transA, transB, va, vb, nb, stream);

@@ -1,0 +1,49 @@
+#pragma once
+// Raw-pointer GEMM launchers (reference include/dl/kernels/gemm.hpp).
+//
+// gemm() keeps the reference's signature and contract: row-major
+// C[m,n] = A[m,k] . B[k,n], C overwritten, null stream.  The GemmAlgo
+// enumerators name this build's gfx950 kernel families; Auto (the default)
+// picks one by shape, as the reference's default picked cuBLAS.
+
+#include <cstddef>
+#include <cstdint>
+
+namespace dl::kernels {
+
+enum class GemmAlgo {
+    Auto,
+    MfmaTiled128,   // 128x128x16 LDS double-buffered fp32 MFMA tile
+    MfmaTiled64,    // 64x64x16 LDS double-buffered fp32 MFMA tile
+    MfmaSplitK,     // 32x32 MFMA tile, K split over the waves of a block
+    Skinny,         // VALU streaming kernel for m <= 8
+};
+
+const char* to_string(GemmAlgo algo);
+
+void gemm(const float* a, const float* b, float* c, int m, int n, int k,
+          GemmAlgo algo = GemmAlgo::Auto);
+
+enum class Transpose { No, Yes };
+
+enum class Epilogue {
+    None,        // C = acc
+    Bias,        // C = acc + bias[j]
+    BiasRelu,    // C = max(0, acc + bias[j])
+    Relu,        // C = max(0, acc)
+    ReluGrad,    // C = aux[i][j] > 0 ? acc : 0
+};
+
+// General strided-batched form (fdl_sgemm_ex in include/fastdl_gemm.h):
+// C[b] = epi(op(A[b]) . op(B[b])), row-major, with leading dimensions and
+// element strides.  `stream` is a hipStream_t (nullptr: null stream).
+// Throws std::runtime_error on invalid arguments or launch failure.
+void gemm_ex(Transpose trans_a, Transpose trans_b, int64_t m, int64_t n, int64_t k,
+             const float* a, int64_t lda, int64_t stride_a,
+             const float* b, int64_t ldb, int64_t stride_b,
+             float* c, int64_t ldc, int64_t stride_c, int64_t batch,
+             const float* bias = nullptr, const float* aux = nullptr,
+             Epilogue epilogue = Epilogue::None, GemmAlgo algo = GemmAlgo::Auto,
+             void* stream = nullptr);
+
+}  // namespace dl::kernels

@@ -1,0 +1,68 @@
+"""The C++ dl:: API: headers, exported symbols (CPU) and the C++ test programs (GPU).
+
+The GPU part runs tests/cpp/bin/api_test (this build's own checks) and the
+reference's own C++ test programs from /root/reference/tests, compiled
+unchanged against this repository's include/dl and libfastdl.so by
+`make -C oracle ref` (oracle/_ref/, built where the reference is mounted and
+shipped prebuilt to the GPU box).  Each prints "<name> : passed".
+"""
+import glob
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+LIB = os.path.join(ROOT, "fast_dl_amd", "libfastdl.so")
+
+PUBLIC_HEADERS = [
+    "dl/dl.hpp", "dl/core/Device.hpp", "dl/core/DType.hpp", "dl/core/Shape.hpp",
+    "dl/tensor/Tensor.hpp", "dl/tensor/TensorImpl.hpp", "dl/ops/Ops.hpp", "dl/ops/OpUtils.hpp",
+    "dl/nn/Module.hpp", "dl/nn/Linear.hpp", "dl/nn/ReLU.hpp", "dl/nn/Sequential.hpp",
+    "dl/kernels/kernels.hpp", "dl/optim/SGD.hpp", "dl/train/Mlp2.hpp",
+]
+
+
+@pytest.mark.parametrize("header", PUBLIC_HEADERS)
+def test_public_headers_are_plain_cxx(header, tmp_path):
+    # No HIP (or CUDA) headers needed to use the API, as in the reference.
+    src = tmp_path / "h.cpp"
+    src.write_text(f"#include <{header}>\nint main() {{ return 0; }}\n")
+    subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", INCLUDE, str(src)], check=True)
+
+
+def test_library_exports_api_symbols():
+    assert os.path.exists(LIB), "libfastdl.so not built"
+    out = subprocess.run(["nm", "-DC", "--defined-only", LIB], capture_output=True, text=True,
+                         check=True).stdout
+    for sym in ["dl::ops::matmul(dl::Tensor const&, dl::Tensor const&)",
+                "dl::ops::linear(dl::Tensor const&, dl::Tensor const&, dl::Tensor const&)",
+                "dl::ops::relu(dl::Tensor const&)",
+                "dl::ops::softmax(dl::Tensor const&)",
+                "dl::ops::cross_entropy(dl::Tensor const&, dl::Tensor const&)",
+                "dl::kernels::gemm(float const*, float const*, float*, int, int, int, "
+                "dl::kernels::GemmAlgo)",
+                "dl::kernels::add_row_bias(float*, float const*, int, int)",
+                "dl::nn::Linear::forward(dl::Tensor const&)",
+                "dl::Tensor::kaiming_uniform(dl::Shape, dl::DType, dl::Device, unsigned long)",
+                "dl::ops::linear_backward("]:
+        assert sym in out, sym
+
+
+def _programs():
+    progs = sorted(glob.glob(os.path.join(ROOT, "tests", "cpp", "bin", "*")))
+    progs += sorted(glob.glob(os.path.join(ROOT, "oracle", "_ref", "*")))
+    return [p for p in progs if os.access(p, os.X_OK) and os.path.isfile(p)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prog", _programs(), ids=lambda p: os.path.relpath(p, ROOT))
+def test_cpp_program(device, prog):
+    print(f"running {prog}", flush=True)
+    proc = subprocess.run([prog], capture_output=True, text=True, timeout=100)
+    print(proc.stdout)
+    print(proc.stderr)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "not passed" not in proc.stdout
+    assert "passed" in proc.stdout

@@ -84,7 +84,11 @@ def test_softmax_fixture_and_random(device):
         capi.softmax(d.data_ptr(), out.data_ptr(), arr.shape[0], arr.shape[1], stream())
         y = host(out)
         ref = oracle.softmax(arr)
-        assert np.max(np.abs(y - ref)) < 1e-6
+        assert np.max(np.abs(y - ref)) < 1e-4  # the reference test's own rule
+        # elementwise: exp differs by a few ulp between libraries and the row sum
+        # by ~sqrt(cols) roundings
+        bound = (8.0 + 2.0 * np.sqrt(arr.shape[1])) * oracle.FLT_EPS * ref + 1e-30
+        assert np.all(np.abs(y - ref) <= bound)
         assert np.all(np.abs(y.sum(1) - 1.0) < 1e-4)
 
 
