@@ -19,6 +19,9 @@ from .capi import (  # noqa: F401
     KERNEL_SPLITK32,
     KERNEL_TILED64,
     KERNEL_TILED128,
+    KERNEL_TILED128W8,
+    KERNEL_TILED256,
+    KERNEL_TILED256X128,
     OP_N,
     OP_T,
     FdlError,

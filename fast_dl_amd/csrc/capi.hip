@@ -36,7 +36,7 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int64_t ldb, int64_t strideB, float* C, int64_t ldc,
                         int64_t strideC, int64_t batch, const float* bias,
                         const float* aux, int epilogue, int kernel, void* stream) {
-    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_SKINNY) {
+    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_TILED128W8) {
         return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
     }
     if ((transA != FDL_OP_N && transA != FDL_OP_T) ||

@@ -32,12 +32,16 @@ struct GemmParams {
     int epilogue;
 };
 
-// Kernel families; the host dispatcher picks one per call.
+// Kernel families; the host dispatcher picks one per call.  Values match
+// fdl_kernel in include/fastdl_gemm.h.
 enum class GemmKernel : int {
-    Tiled128 = 0,   // 128x128x16 LDS double-buffered MFMA tile
-    Tiled64 = 1,    // 64x64x16 LDS double-buffered MFMA tile
-    SplitK32 = 2,   // 32x32 output tile, K split over the waves of a block
-    Skinny = 3,     // VALU strip kernel for M <= 8 with B not transposed
+    Tiled128 = 0,     // 128x128x16 tile, 4 waves of 64x64
+    Tiled64 = 1,      // 64x64x16 tile, 4 waves of 32x32
+    SplitK32 = 2,     // 32x32 output tile, K split over the waves of a block
+    Skinny = 3,       // VALU strip kernel for M <= 8 with B not transposed
+    Tiled256 = 4,     // 256x256x16 tile, 8 waves of 128x64
+    Tiled256x128 = 5, // 256x128x16 tile, 8 waves of 64x64
+    Tiled128W8 = 6,   // 128x128x16 tile, 8 waves of 32x64
     Auto = -1,
 };
 

@@ -588,6 +588,45 @@ constexpr int kMaxGridY = 65535;
 // Production tile configurations (BM, BN, BK, WM, WN, PAD, waves per SIMD).
 using CfgTiled128 = TileCfg<128, 128, 16, 64, 64, 4, 1>;
 using CfgTiled64 = TileCfg<64, 64, 16, 32, 32, 4, 1>;
+using CfgTiled256 = TileCfg<256, 256, 16, 128, 64, 4, 1>;
+using CfgTiled256x128 = TileCfg<256, 128, 16, 64, 64, 4, 1>;
+using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
+
+// Dispatch cost model.  A config runs `slots` blocks per CU at full
+// occupancy (LDS and register bound), each block holding `waves` waves; eff[w]
+// is the measured fraction of fp32-MFMA peak a CU reaches with w resident
+// waves per SIMD (w = 1..8).  The predicted time of a problem is the time of
+// the most loaded CU: its tiles run in rounds of up to `slots` co-resident
+// blocks, each round costing (tiles in round) * BM * BN / eff[w].
+struct TileModel {
+    GemmKernel kernel;
+    int bm, bn, slots, waves;
+    float eff[9];
+};
+
+constexpr TileModel kTileModels[] = {
+    {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
+    {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
+    {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.72f, 0.80f, 0.80f, 0.80f, 0.80f, 0.80f, 0.80f}},
+    {GemmKernel::Tiled128W8, 128, 128, 3, 8, {0, 0.45f, 0.63f, 0.68f, 0.72f, 0.74f, 0.75f, 0.75f, 0.75f}},
+    {GemmKernel::Tiled64, 64, 64, 8, 4, {0, 0.30f, 0.45f, 0.52f, 0.60f, 0.63f, 0.65f, 0.67f, 0.68f}},
+};
+
+double predicted_time(const TileModel& t, int M, int N, int64_t batch) {
+    constexpr int64_t kCUs = 256;
+    const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
+    const int64_t per_cu = (tiles + kCUs - 1) / kCUs;
+    const double work = (double)t.bm * t.bn;
+    const int64_t full = per_cu / t.slots;
+    const int64_t rest = per_cu % t.slots;
+    auto round_cost = [&](int64_t blocks) {
+        const int w = (int)std::min<int64_t>(8, std::max<int64_t>(1, blocks * t.waves / 4));
+        return (double)blocks * work / t.eff[w];
+    };
+    double time = (double)full * round_cost(t.slots);
+    if (rest) time += round_cost(rest);
+    return time;
+}
 
 }  // namespace
 
@@ -597,6 +636,9 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::Tiled64: return "tiled64";
         case GemmKernel::SplitK32: return "splitk32";
         case GemmKernel::Skinny: return "skinny";
+        case GemmKernel::Tiled256: return "tiled256";
+        case GemmKernel::Tiled256x128: return "tiled256x128";
+        case GemmKernel::Tiled128W8: return "tiled128w8";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -608,12 +650,23 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     // Skinny M: one streaming pass over B on the VALU beats an MFMA tile
     // that would be at most 8/32 occupied.
     if (p.M <= 8 && !transB && p.N >= 64) return GemmKernel::Skinny;
-    const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     const int64_t t64 = (int64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
     constexpr int64_t kCUs = 256;
-    if (t128 >= 2 * kCUs) return GemmKernel::Tiled128;
-    if (t64 >= kCUs && p.K >= 64) return GemmKernel::Tiled64;
-    return GemmKernel::SplitK32;
+    // Too few 64x64 tiles to occupy the GPU, or too short a K loop to
+    // amortise LDS staging: split K over the waves of a block instead.
+    if (t64 < kCUs || p.K < 64) return GemmKernel::SplitK32;
+    GemmKernel best = GemmKernel::Tiled64;
+    double best_time = 0.0;
+    bool first = true;
+    for (const TileModel& t : kTileModels) {
+        const double tm = predicted_time(t, p.M, p.N, batch);
+        if (first || tm < best_time * 0.99) {  // ties keep the earlier (larger) tile
+            best = t.kernel;
+            best_time = tm;
+            first = false;
+        }
+    }
+    return best;
 }
 
 hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
@@ -639,6 +692,15 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::Tiled64:
                 err = launch_tiled<CfgTiled64>(p, transA, transB, va, vb, nb, stream);
+                break;
+            case GemmKernel::Tiled256:
+                err = launch_tiled<CfgTiled256>(p, transA, transB, va, vb, nb, stream);
+                break;
+            case GemmKernel::Tiled256x128:
+                err = launch_tiled<CfgTiled256x128>(p, transA, transB, va, vb, nb, stream);
+                break;
+            case GemmKernel::Tiled128W8:
+                err = launch_tiled<CfgTiled128W8>(p, transA, transB, va, vb, nb, stream);
                 break;
             case GemmKernel::SplitK32:
                 err = launch_splitk32(p, transA, transB, va, vb, nb, stream);

@@ -87,10 +87,13 @@ int fdl_sgemm_ex(int transA, int transB,
  * reference, include/dl/kernels/gemm.hpp:7-12; the set is this build's own). */
 typedef enum fdl_kernel {
     FDL_KERNEL_AUTO = -1,      /* size heuristic (what fdl_sgemm_ex uses)       */
-    FDL_KERNEL_TILED128 = 0,   /* 128x128x16 LDS double-buffered MFMA tile      */
-    FDL_KERNEL_TILED64 = 1,    /* 64x64x16 LDS double-buffered MFMA tile        */
-    FDL_KERNEL_SPLITK32 = 2,   /* 32x32 MFMA tile, K split over 8 waves          */
-    FDL_KERNEL_SKINNY = 3      /* VALU strip kernel, M <= 8 and transB == N     */
+    FDL_KERNEL_TILED128 = 0,   /* 128x128x16 LDS double-buffered MFMA tile, 4 waves */
+    FDL_KERNEL_TILED64 = 1,    /* 64x64x16 LDS double-buffered MFMA tile, 4 waves   */
+    FDL_KERNEL_SPLITK32 = 2,   /* 32x32 MFMA tile, K split over 8 waves              */
+    FDL_KERNEL_SKINNY = 3,     /* VALU strip kernel, M <= 8 and transB == N         */
+    FDL_KERNEL_TILED256 = 4,   /* 256x256x16 LDS double-buffered MFMA tile, 8 waves */
+    FDL_KERNEL_TILED256X128 = 5, /* 256x128x16 tile, 8 waves                        */
+    FDL_KERNEL_TILED128W8 = 6  /* 128x128x16 tile, 8 waves of 32x64                 */
 } fdl_kernel;
 
 /*

@@ -17,7 +17,8 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, say, stream
 
 pytestmark = pytest.mark.gpu
 
-FAMILIES = [capi.KERNEL_TILED128, capi.KERNEL_TILED64, capi.KERNEL_SPLITK32]
+FAMILIES = [capi.KERNEL_TILED128, capi.KERNEL_TILED64, capi.KERNEL_SPLITK32,
+            capi.KERNEL_TILED256, capi.KERNEL_TILED256X128, capi.KERNEL_TILED128W8]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 
 
@@ -262,6 +263,6 @@ def test_degenerate_sizes(device):
 
 
 def test_kernel_choice_heuristic(device):
-    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED128
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED256
     assert capi.kernel_choice(0, 0, 1, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 1, 4096, 4096) != capi.KERNEL_SKINNY
