@@ -208,7 +208,29 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
         return fail(FDL_ERROR_INVALID_VALUE, "mlp2_train_step: null pointer");
     }
     const int64_t B = batch, I = in_features, Hd = hidden, Cc = classes;
+    const hipStream_t hs = as_stream(stream);
     int st;
+    // Weight-gradient GEMM with the SGD step fused: dW = op(A) op(B) and
+    // W -= lr * dW in the epilogue (the gradient is still written to dW).
+    auto grad_and_step = [&](bool ta, bool tb, int64_t M, int64_t N, int64_t K,
+                             const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                             float* dW, float* W) {
+        fdl::GemmParams p{};
+        p.A = A;
+        p.B = Bm;
+        p.C = dW;
+        p.upd = W;
+        p.lr = lr;
+        p.lda = lda;
+        p.ldb = ldb;
+        p.ldc = N;
+        p.M = (int)M;
+        p.N = (int)N;
+        p.K = (int)K;
+        p.epilogue = fdl::EPI_SGD;
+        return check_hip(fdl::launch_sgemm(p, ta, tb, 1, fdl::GemmKernel::Auto, hs),
+                         "mlp2_train_step weight update failed");
+    };
     // Forward: H = relu(X W1 + b1), logits = H W2 + b2.
     st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Hd, I, X, I, 0, W1, Hd, 0, H, Hd, 0, 1, b1,
                       nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
@@ -216,36 +238,39 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
     st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Cc, Hd, H, Hd, 0, W2, Cc, 0, logits, Cc, 0, 1,
                       b2, nullptr, FDL_EPILOGUE_BIAS, stream);
     if (st) return st;
-    // Loss and dL/dlogits.
-    st = fdl_softmax_xent(logits, labels, loss, G2, B, Cc, stream);
-    if (st) return st;
-    // Layer 2 backward: dW2 = H^T G2 (TN), db2 = colsum(G2),
-    // G1 = (G2 W2^T) masked by H > 0 (NT with the ReLU-gradient epilogue).
-    st = fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, Hd, Cc, B, H, Hd, 0, G2, Cc, 0, dW2, Cc, 0, 1,
-                      nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
-    if (st) return st;
-    st = fdl_colsum(G2, db2, B, Cc, stream);
-    if (st) return st;
+    // Loss, G2 = dL/dlogits, db2 = colsum(G2) and b2 -= lr * db2 in one kernel
+    // (two launches when the class count is too large to stage in LDS).
+    if (Cc <= fdl::kXentFusedMaxClasses) {
+        st = check_hip(fdl::launch_softmax_xent_db_sgd(logits, labels, loss, G2, db2, b2, lr, B,
+                                                       Cc, hs),
+                       "mlp2_train_step loss failed");
+        if (st) return st;
+    } else {
+        st = fdl_softmax_xent(logits, labels, loss, G2, B, Cc, stream);
+        if (st) return st;
+        st = check_hip(fdl::launch_colsum_sgd(G2, db2, b2, lr, B, Cc, hs),
+                       "mlp2_train_step db2 failed");
+        if (st) return st;
+    }
+    // G1 = (G2 W2^T) masked by H > 0 (NT GEMM, ReLU-gradient epilogue); this
+    // reads W2 before its update below.
     st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, Hd, Cc, G2, Cc, 0, W2, Cc, 0, G1, Hd, 0, 1,
                       nullptr, H, FDL_EPILOGUE_RELU_GRAD, stream);
     if (st) return st;
-    // Layer 1 backward: dW1 = X^T G1 (TN), db1 = colsum(G1), dX = G1 W1^T (NT).
-    st = fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, I, Hd, B, X, I, 0, G1, Hd, 0, dW1, Hd, 0, 1,
-                      nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
+    // dW2 = H^T G2 (TN) and W2 -= lr * dW2.
+    st = grad_and_step(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2, W2);
     if (st) return st;
-    st = fdl_colsum(G1, db1, B, Hd, stream);
-    if (st) return st;
+    // dX = G1 W1^T (NT), before W1 changes.
     if (dX) {
         st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, I, Hd, G1, Hd, 0, W1, Hd, 0, dX, I, 0, 1,
                           nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
         if (st) return st;
     }
-    // SGD on all four parameters in one launch.
-    float* params[4] = {W1, b1, W2, b2};
-    const float* grads[4] = {dW1, db1, dW2, db2};
-    const int64_t sizes[4] = {I * Hd, Hd, Hd * Cc, Cc};
-    return check_hip(fdl::launch_sgd_multi(4, params, grads, sizes, lr, as_stream(stream)),
-                     "mlp2_train_step sgd launch failed");
+    // dW1 = X^T G1 (TN) and W1 -= lr * dW1; db1 = colsum(G1) and b1 -= lr * db1.
+    st = grad_and_step(true, false, I, Hd, B, X, I, G1, Hd, dW1, W1);
+    if (st) return st;
+    return check_hip(fdl::launch_colsum_sgd(G1, db1, b1, lr, B, Hd, hs),
+                     "mlp2_train_step db1 failed");
 }
 
 int fdl_fill_uniform(float* data, int64_t n, float low, float high, uint64_t seed,

@@ -16,6 +16,9 @@ enum Epilogue : int {
     EPI_BIAS_RELU = 2,
     EPI_RELU = 3,
     EPI_RELU_GRAD = 4,
+    // Internal (not in the C-ABI enum): C = v and upd[i][j] -= lr * v, i.e. a
+    // weight-gradient GEMM that also applies the SGD step to the weight.
+    EPI_SGD = 5,
 };
 
 // One strided-batched GEMM problem, already validated on the host.
@@ -26,6 +29,8 @@ struct GemmParams {
     float* C;
     const float* bias;  // length N, or null
     const float* aux;   // same layout as C (ldc, strideC), or null
+    float* upd;         // EPI_SGD: parameter updated in place, same layout as C
+    float lr;           // EPI_SGD: learning rate
     int64_t lda, ldb, ldc;
     int64_t strideA, strideB, strideC;
     int M, N, K;
@@ -64,11 +69,22 @@ hipError_t launch_relu_backward(const float* g, const float* act, float* out,
                                 int64_t n, hipStream_t stream);
 hipError_t launch_colsum(const float* x, float* out, int64_t rows, int64_t cols,
                          hipStream_t stream);
+// out = column sums of x, then param -= lr * out (param may be null).
+hipError_t launch_colsum_sgd(const float* x, float* out, float* param, float lr,
+                             int64_t rows, int64_t cols, hipStream_t stream);
 hipError_t launch_softmax(const float* in, float* out, int64_t rows,
                           int64_t cols, hipStream_t stream);
 hipError_t launch_softmax_xent(const float* logits, const int64_t* labels,
                                float* loss, float* grad, int64_t batch,
                                int64_t classes, hipStream_t stream);
+// As launch_softmax_xent, and also db = column sums of the gradient and
+// bparam -= lr * db (the bias step of the layer that produced the logits).
+// Needs grad, db and bparam; classes <= kXentFusedMaxClasses.
+constexpr int kXentFusedMaxClasses = 32;
+hipError_t launch_softmax_xent_db_sgd(const float* logits, const int64_t* labels,
+                                      float* loss, float* grad, float* db, float* bparam,
+                                      float lr, int64_t batch, int64_t classes,
+                                      hipStream_t stream);
 hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,
                       hipStream_t stream);
 // Up to four (param, grad, n) updates in one launch.

@@ -46,26 +46,43 @@ __global__ void relu_backward_kernel(const float* __restrict__ g,
     }
 }
 
-// Column sums, rows added in increasing order by one thread per column.
-// A block covers 64 columns x 4 row groups; the 4 group partials are added
-// in group order, so the result is deterministic.
-__global__ void colsum_kernel(const float* __restrict__ x, float* __restrict__ out,
-                              int64_t rows, int64_t cols) {
-    __shared__ float part[4][64];
-    const int c_local = threadIdx.x & 63;
-    const int grp = threadIdx.x >> 6;
-    const int64_t c = blockIdx.x * 64 + c_local;
-    const int64_t per = (rows + 3) / 4;
-    const int64_t r0 = grp * per;
-    const int64_t r1 = std::min<int64_t>(rows, r0 + per);
+// Column sums.  A block owns 32 columns; its 8 row groups each add every 8th
+// row (unrolled so eight independent loads are in flight per thread), and the
+// 8 group partials are added in group order: deterministic run to run.
+// With `param`, the block also applies param[c] -= lr * sum (SGD on a bias).
+constexpr int kColsumCols = 32;
+constexpr int kColsumGroups = 8;
+
+__global__ void __launch_bounds__(kColsumCols * kColsumGroups)
+colsum_kernel(const float* __restrict__ x, float* __restrict__ out,
+              float* __restrict__ param, float lr, int64_t rows, int64_t cols) {
+#pragma clang fp contract(off)
+    __shared__ float part[kColsumGroups][kColsumCols];
+    const int cl = threadIdx.x % kColsumCols;
+    const int grp = threadIdx.x / kColsumCols;
+    const int64_t c = blockIdx.x * (int64_t)kColsumCols + cl;
+    const int64_t cc = c < cols ? c : cols - 1;  // clamped: loads stay in bounds
     float s = 0.0f;
-    if (c < cols) {
-        for (int64_t r = r0; r < r1; ++r) s += x[r * cols + c];
+    int64_t r = grp;
+    for (; r + 7 * kColsumGroups < rows; r += 8 * kColsumGroups) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = x[(r + u * kColsumGroups) * cols + cc];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
     }
-    part[grp][c_local] = s;
+    for (; r < rows; r += kColsumGroups) s += x[r * cols + cc];
+    part[grp][cl] = s;
     __syncthreads();
     if (grp == 0 && c < cols) {
-        out[c] = ((part[0][c_local] + part[1][c_local]) + part[2][c_local]) + part[3][c_local];
+        float t = part[0][cl];
+#pragma unroll
+        for (int g = 1; g < kColsumGroups; ++g) t += part[g][cl];
+        out[c] = t;
+        if (param) {
+            const float step = lr * t;
+            param[c] = param[c] - step;
+        }
     }
 }
 
@@ -138,6 +155,69 @@ softmax_xent_kernel(const float* __restrict__ logits,
 
 // p -= lr * g with the product rounded before the subtraction (no FMA
 // contraction), as the reference's x86 host update computes it.
+// Softmax cross-entropy for classes <= kXentFusedMaxClasses with the bias
+// gradient and the bias SGD step fused: one block walks the batch in chunks of
+// 256 rows staged through LDS with coalesced loads (thread t owns row t of
+// the chunk), writes the gradient through LDS with coalesced stores, and adds
+// each chunk's gradient column sums in row order.  db and bparam are written
+// once at the end.
+__global__ void __launch_bounds__(kBlock)
+softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
+                           const int64_t* __restrict__ labels, float* __restrict__ loss,
+                           float* __restrict__ grad, float* __restrict__ db,
+                           float* __restrict__ bparam, float lr, int64_t batch,
+                           int64_t classes) {
+#pragma clang fp contract(off)
+    __shared__ float zs[kBlock * kXentFusedMaxClasses];
+    __shared__ float part[kBlock];
+    const int t = threadIdx.x;
+    const float inv_b = 1.0f / (float)batch;
+    float lsum = 0.0f;
+    float dbc = 0.0f;  // running column sum for class t (t < classes)
+    for (int64_t r0 = 0; r0 < batch; r0 += kBlock) {
+        const int rows = (int)min<int64_t>(kBlock, batch - r0);
+        const int n = rows * (int)classes;
+        const float* zsrc = logits + r0 * classes;
+        for (int e = t; e < n; e += kBlock) zs[e] = zsrc[e];
+        __syncthreads();
+        if (t < rows) {
+            float* z = zs + t * classes;
+            float mx = z[0];
+            for (int c = 1; c < classes; ++c) mx = fmaxf(mx, z[c]);
+            float s = 0.0f;
+            for (int c = 0; c < classes; ++c) s += expf(z[c] - mx);
+            const int64_t label = labels[r0 + t];
+            const bool valid = label >= 0 && label < classes;
+            if (valid) lsum += (logf(s) + mx - z[label]) * inv_b;
+            const float inv_s = 1.0f / s;
+            for (int c = 0; c < classes; ++c) {
+                float pc = expf(z[c] - mx) * inv_s;
+                if (valid && c == label) pc -= 1.0f;
+                z[c] = pc * inv_b;
+            }
+        }
+        __syncthreads();
+        float* gdst = grad + r0 * classes;
+        for (int e = t; e < n; e += kBlock) gdst[e] = zs[e];
+        if (t < classes) {
+            for (int r = 0; r < rows; ++r) dbc += zs[r * classes + t];
+        }
+        __syncthreads();
+    }
+    if (t < classes) {
+        db[t] = dbc;
+        const float step = lr * dbc;
+        bparam[t] = bparam[t] - step;
+    }
+    part[t] = lsum;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if (t < w) part[t] += part[t + w];
+        __syncthreads();
+    }
+    if (t == 0 && loss) loss[0] = part[0];
+}
+
 __global__ void sgd_kernel(float* __restrict__ p, const float* __restrict__ g,
                            float lr, int64_t n) {
 #pragma clang fp contract(off)
@@ -251,13 +331,18 @@ hipError_t launch_relu_backward(const float* g, const float* act, float* out,
     return hipGetLastError();
 }
 
+hipError_t launch_colsum_sgd(const float* x, float* out, float* param, float lr,
+                             int64_t rows, int64_t cols, hipStream_t stream) {
+    if (cols == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((cols + kColsumCols - 1) / kColsumCols);
+    hipLaunchKernelGGL(colsum_kernel, dim3(blocks), dim3(kColsumCols * kColsumGroups), 0,
+                       stream, x, out, param, lr, rows, cols);
+    return hipGetLastError();
+}
+
 hipError_t launch_colsum(const float* x, float* out, int64_t rows, int64_t cols,
                          hipStream_t stream) {
-    if (cols == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)((cols + 63) / 64);
-    hipLaunchKernelGGL(colsum_kernel, dim3(blocks), dim3(kBlock), 0, stream, x,
-                       out, rows, cols);
-    return hipGetLastError();
+    return launch_colsum_sgd(x, out, nullptr, 0.0f, rows, cols, stream);
 }
 
 hipError_t launch_softmax(const float* in, float* out, int64_t rows, int64_t cols,
@@ -274,6 +359,16 @@ hipError_t launch_softmax_xent(const float* logits, const int64_t* labels,
                                int64_t classes, hipStream_t stream) {
     hipLaunchKernelGGL(softmax_xent_kernel, dim3(1), dim3(kBlock), 0, stream,
                        logits, labels, loss, grad, batch, classes);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_xent_db_sgd(const float* logits, const int64_t* labels,
+                                      float* loss, float* grad, float* db, float* bparam,
+                                      float lr, int64_t batch, int64_t classes,
+                                      hipStream_t stream) {
+    if (classes > kXentFusedMaxClasses || !grad || !db || !bparam) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(softmax_xent_db_sgd_kernel, dim3(1), dim3(kBlock), 0, stream, logits,
+                       labels, loss, grad, db, bparam, lr, batch, classes);
     return hipGetLastError();
 }
 

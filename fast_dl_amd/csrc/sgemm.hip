@@ -38,22 +38,37 @@ __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m,
     tn = in_group / gsize;
 }
 
-__device__ __forceinline__ float apply_epilogue(float v, int epi,
-                                                const float* __restrict__ bias,
-                                                const float* __restrict__ aux,
-                                                int64_t c_off, int j) {
-    switch (epi) {
+// Applies the epilogue to accumulator v of element (., j) at offset off and
+// stores it.  EPI_SGD also updates the parameter: upd -= lr * v, with the
+// product rounded before the subtraction as in the reference's host update.
+__device__ __forceinline__ void store_epilogue(float v, const GemmParams& p,
+                                               float* __restrict__ C,
+                                               const float* __restrict__ aux,
+                                               float* __restrict__ upd, int64_t off,
+                                               int j) {
+#pragma clang fp contract(off)
+    switch (p.epilogue) {
         case EPI_BIAS:
-            return v + bias[j];
+            v = v + p.bias[j];
+            break;
         case EPI_BIAS_RELU:
-            return fmaxf(0.0f, v + bias[j]);
+            v = fmaxf(0.0f, v + p.bias[j]);
+            break;
         case EPI_RELU:
-            return fmaxf(0.0f, v);
+            v = fmaxf(0.0f, v);
+            break;
         case EPI_RELU_GRAD:
-            return aux[c_off] > 0.0f ? v : 0.0f;
+            v = aux[off] > 0.0f ? v : 0.0f;
+            break;
+        case EPI_SGD: {
+            const float step = p.lr * v;
+            upd[off] = upd[off] - step;
+            break;
+        }
         default:
-            return v;
+            break;
     }
+    C[off] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -144,10 +159,12 @@ struct TileLoader {
 // per LDS row; WPE is the minimum number of waves per SIMD the register
 // allocation must allow (occupancy target).
 // ---------------------------------------------------------------------------
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int PAD_, int WPE_, int PRIO_ = 0>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int PAD_, int WPE_, int PRIO_ = 0,
+          int KCH_ = BK_ / 2, int STORE_MID_ = 0, int PIPE_ = 0>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-    static constexpr int PAD = PAD_, WPE = WPE_, PRIO = PRIO_;
+    static constexpr int PAD = PAD_, WPE = WPE_, PRIO = PRIO_, KCH = KCH_, STORE_MID = STORE_MID_;
+    static constexpr int PIPE = PIPE_;
     static constexpr int NT = kWave * (BM / WM) * (BN / WN);
 };
 
@@ -216,32 +233,64 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
             }
             const float* __restrict__ as = As[cur];
             const float* __restrict__ bs = Bs[cur];
-            // Read every operand fragment of this K-tile before the first MFMA,
-            // so the LDS latency is paid once per tile rather than per k pair.
-            float a[BK / 2][FM];
-            float b[BK / 2][FN];
+            // Operand fragments are read from LDS a chunk of KCH k pairs at a
+            // time, all before the chunk's first MFMA, so the LDS latency is
+            // paid once per chunk rather than per k pair.  With STORE_MID the
+            // prefetched next tile is written to the other LDS buffer halfway
+            // through the MFMAs instead of after them.
+            constexpr int KP = BK / 2;
+            constexpr int KCH = Cfg::KCH;
+            constexpr int NCH = KP / KCH;
+            static_assert(KP % KCH == 0, "chunk must divide the k pairs of a tile");
+            // Double-buffered fragment registers: with PIPE the reads of chunk
+            // c+1 are issued before the MFMAs of chunk c.
+            float a[2][KCH][FM];
+            float b[2][KCH][FN];
+            auto read_chunk = [&](int c, int slot) {
 #pragma unroll
-            for (int kp = 0; kp < BK / 2; ++kp) {
+                for (int q = 0; q < KCH; ++q) {
+                    const int kk = 2 * (c * KCH + q) + half;
 #pragma unroll
-                for (int mi = 0; mi < FM; ++mi)
-                    a[kp][mi] = as[(2 * kp + half) * LoaderA::LD + wm0 + mi * 32 + l32];
-#pragma unroll
-                for (int ni = 0; ni < FN; ++ni)
-                    b[kp][ni] = bs[(2 * kp + half) * LoaderB::LD + wn0 + ni * 32 + l32];
-            }
-            // Keep the scheduler from sinking the reads back next to their MFMAs.
-            __builtin_amdgcn_sched_barrier(0);
-            if (Cfg::PRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int kp = 0; kp < BK / 2; ++kp)
-#pragma unroll
-                for (int mi = 0; mi < FM; ++mi)
+                    for (int mi = 0; mi < FM; ++mi)
+                        a[slot][q][mi] = as[kk * LoaderA::LD + wm0 + mi * 32 + l32];
 #pragma unroll
                     for (int ni = 0; ni < FN; ++ni)
-                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            a[kp][mi], b[kp][ni], acc[mi][ni], 0, 0, 0);
-            if (Cfg::PRIO) __builtin_amdgcn_s_setprio(0);
-            if (has_next) {
+                        b[slot][q][ni] = bs[kk * LoaderB::LD + wn0 + ni * 32 + l32];
+                }
+            };
+            if (Cfg::PIPE) read_chunk(0, 0);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int slot = Cfg::PIPE ? (c & 1) : 0;
+                if (Cfg::PIPE) {
+                    if (c + 1 < NCH) read_chunk(c + 1, slot ^ 1);
+                } else {
+                    read_chunk(c, 0);
+                }
+                // Keep the scheduler from sinking the reads back next to their MFMAs.
+                __builtin_amdgcn_sched_barrier(0);
+                if (Cfg::PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int q = 0; q < KCH; ++q) {
+                    if (Cfg::STORE_MID && c * KCH + q == KP / 2) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (has_next) {
+                            la.store(As[cur ^ 1], tid);
+                            lb.store(Bs[cur ^ 1], tid);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                        for (int ni = 0; ni < FN; ++ni)
+                            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                a[slot][q][mi], b[slot][q][ni], acc[mi][ni], 0, 0, 0);
+                }
+                if (Cfg::PRIO) __builtin_amdgcn_s_setprio(0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (!Cfg::STORE_MID && has_next) {
                 la.store(As[cur ^ 1], tid);
                 lb.store(Bs[cur ^ 1], tid);
             }
@@ -251,6 +300,7 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 
     float* __restrict__ C = p.C + bz * p.strideC;
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
     const int epi = p.epilogue;
     const bool has_bias = epi == EPI_BIAS || epi == EPI_BIAS_RELU;
     const bool relu = epi == EPI_BIAS_RELU || epi == EPI_RELU;
@@ -271,6 +321,11 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
                     if (has_bias) v += bj;
                     if (relu) v = fmaxf(0.0f, v);
                     if (epi == EPI_RELU_GRAD) v = aux[off] > 0.0f ? v : 0.0f;
+                    if (epi == EPI_SGD) {
+#pragma clang fp contract(off)
+                        const float step = p.lr * v;
+                        upd[off] = upd[off] - step;
+                    }
                     C[off] = v;
                 }
             }
@@ -284,10 +339,69 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // the k index permuted inside each group of 8: at step s (0..3) the lane in
 // half h supplies k = k0 + 4h + s, so one lane's four A values are contiguous
 // (a 16-byte load when A is k-contiguous).  The permutation is applied to A
-// and B alike, so the four MFMAs still cover k0..k0+7 exactly once.  Partial
-// 32x32 sums meet in LDS and are added in wave order, then the epilogue runs.
+// and B alike, so the four MFMAs still cover k0..k0+7 exactly once.
+// Groups are loaded ITS at a time into one of two register buffers: the loads
+// of the next ITS groups are in flight while the MFMAs of the current ones
+// run, so a wave pays the global-load latency about once per ITS groups
+// instead of once per group.  Partial 32x32 sums meet in LDS and are added
+// in wave order, then the epilogue runs.
 // ---------------------------------------------------------------------------
-template <int KW, bool TA, bool TB, bool VA, bool VB>
+// One group of 8 reduction steps for this lane.  `row` and `col` are already
+// clamped into the matrix: a lane whose row (column) lies outside C loads a
+// valid row and only pollutes accumulator rows (columns) that are never
+// stored, so no select is needed and every load is issued unconditionally.
+// With `tail`, k indices at or past kend are clamped and their values zeroed.
+template <bool TA, bool TB, bool VA, bool VB>
+__device__ __forceinline__ void splitk_load_group(const float* __restrict__ A,
+                                                  const float* __restrict__ B,
+                                                  const GemmParams& p, int row, int col,
+                                                  int kb, int kend, bool tail, float a[4],
+                                                  float b[4]) {
+    if (!tail) {
+        if (!TA) {
+            const float* ar = A + (int64_t)row * p.lda + kb;
+            if (VA) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(ar);
+                a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) a[s] = ar[s];
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) a[s] = A[(int64_t)(kb + s) * p.lda + row];
+        }
+        if (TB) {
+            const float* br = B + (int64_t)col * p.ldb + kb;
+            if (VB) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(br);
+                b[0] = v[0]; b[1] = v[1]; b[2] = v[2]; b[3] = v[3];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) b[s] = br[s];
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) b[s] = B[(int64_t)(kb + s) * p.ldb + col];
+        }
+    } else {
+        float av[4], bv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kk = kb + s < kend ? kb + s : 0;
+            av[s] = TA ? A[(int64_t)kk * p.lda + row] : A[(int64_t)row * p.lda + kk];
+            bv[s] = TB ? B[(int64_t)col * p.ldb + kk] : B[(int64_t)kk * p.ldb + col];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const bool kin = kb + s < kend;
+            a[s] = kin ? av[s] : 0.0f;
+            b[s] = kin ? bv[s] : 0.0f;
+        }
+    }
+}
+
+template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
 __global__ void __launch_bounds__(KW * 64)
 sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     __shared__ float red[KW][16][kWave];
@@ -306,68 +420,52 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
 
-    const int row = m0 + i;  // row of op(A) this lane feeds
-    const int col = n0 + i;  // column of op(B) this lane feeds
-    const bool row_ok = row < p.M;
-    const bool col_ok = col < p.N;
+    // Row of op(A) and column of op(B) this lane feeds, clamped into the
+    // matrix (see splitk_load_group).
+    const int row = min(m0 + i, p.M - 1);
+    const int col = min(n0 + i, p.N - 1);
     const int kbeg = wave * kchunk;
     const int kend = min(p.K, kbeg + kchunk);
+    const int groups = kend > kbeg ? (kend - kbeg + 7) / 8 : 0;
+    const int supers = (groups + ITS - 1) / ITS;
 
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 
-    for (int k = kbeg; k < kend; k += 8) {
-        const int kb = k + 4 * h;
-        float a[4];
-        float b[4];
-        if (k + 8 <= kend) {
-            if (!TA) {
-                const float* ar = A + (int64_t)row * p.lda + kb;
-                if (VA) {
-                    floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (row_ok) v = *reinterpret_cast<const floatx4*>(ar);
-                    a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
-                } else {
+    float a0[ITS][4], b0[ITS][4], a1[ITS][4], b1[ITS][4];
+    // Groups past the wave's range load as zeros, so a super-chunk always
+    // issues ITS groups of MFMAs.
+    auto load_super = [&](int sc, float (&a)[ITS][4], float (&b)[ITS][4]) {
+        const int k0 = kbeg + 8 * sc * ITS;
+        if (k0 + 8 * ITS <= kend) {  // wave-uniform: the whole super-chunk is in range
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) a[s] = row_ok ? ar[s] : 0.0f;
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    a[s] = row_ok ? A[(int64_t)(kb + s) * p.lda + row] : 0.0f;
-            }
-            if (TB) {
-                const float* br = B + (int64_t)col * p.ldb + kb;
-                if (VB) {
-                    floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (col_ok) v = *reinterpret_cast<const floatx4*>(br);
-                    b[0] = v[0]; b[1] = v[1]; b[2] = v[2]; b[3] = v[3];
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) b[s] = col_ok ? br[s] : 0.0f;
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    b[s] = col_ok ? B[(int64_t)(kb + s) * p.ldb + col] : 0.0f;
-            }
+            for (int q = 0; q < ITS; ++q)
+                splitk_load_group<TA, TB, VA, VB>(A, B, p, row, col, k0 + 8 * q + 4 * h, kend,
+                                                  false, a[q], b[q]);
         } else {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int kk = kb + s;
-                const bool kin = kk < kend;
-                a[s] = (row_ok && kin)
-                           ? (TA ? A[(int64_t)kk * p.lda + row] : A[(int64_t)row * p.lda + kk])
-                           : 0.0f;
-                b[s] = (col_ok && kin)
-                           ? (TB ? B[(int64_t)col * p.ldb + kk] : B[(int64_t)kk * p.ldb + col])
-                           : 0.0f;
-            }
+            for (int q = 0; q < ITS; ++q)
+                splitk_load_group<TA, TB, VA, VB>(A, B, p, row, col, k0 + 8 * q + 4 * h, kend,
+                                                  true, a[q], b[q]);
         }
+    };
+    auto mfma_super = [&](const float (&a)[ITS][4], const float (&b)[ITS][4]) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
+        for (int q = 0; q < ITS; ++q)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q][s], b[q][s], acc, 0, 0, 0);
+    };
+
+    if (supers > 0) load_super(0, a0, b0);
+    for (int sc = 0; sc < supers; sc += 2) {
+        if (sc + 1 < supers) load_super(sc + 1, a1, b1);
+        mfma_super(a0, b0);
+        if (sc + 1 < supers) {
+            if (sc + 2 < supers) load_super(sc + 2, a0, b0);
+            mfma_super(a1, b1);
+        }
     }
 
 #pragma unroll
@@ -376,6 +474,7 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 
     float* __restrict__ C = p.C + bz * p.strideC;
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
     for (int e = tid; e < 16 * kWave; e += KW * kWave) {
         const int r = e / kWave;
         const int ln = e % kWave;
@@ -386,7 +485,7 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
         const int gj = n0 + (ln & 31);
         if (gi < p.M && gj < p.N) {
             const int64_t off = (int64_t)gi * p.ldc + gj;
-            C[off] = apply_epilogue(v, p.epilogue, p.bias, aux, off, gj);
+            store_epilogue(v, p, C, aux, upd, off, gj);
         }
     }
 }
@@ -457,6 +556,7 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
 
     float* __restrict__ C = p.C + bz * p.strideC;
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
     for (int e = tid; e < MR * STRIP; e += NT) {
         const int m = e / STRIP;
         const int c = e % STRIP;
@@ -465,7 +565,7 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
             float v = 0.0f;
             for (int q = 0; q < KL; ++q) v += red[q][m][c];
             const int64_t off = (int64_t)m * p.ldc + j;
-            C[off] = apply_epilogue(v, p.epilogue, p.bias, aux, off, j);
+            store_epilogue(v, p, C, aux, upd, off, j);
         }
     }
 }
@@ -522,14 +622,17 @@ hipError_t launch_tiled(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
     return hipGetLastError();
 }
 
-hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
-                           int nbatch, hipStream_t stream) {
-    constexpr int KW = 8;
+template <int KW>
+hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
+                              int nbatch, hipStream_t stream) {
+    constexpr int ITS = 4;
     const int tiles_m = (p.M + 31) / 32;
     const int tiles_n = (p.N + 31) / 32;
-    // K range per wave, a multiple of 8 (one MFMA group).
+    // K range per wave, a multiple of one super-chunk (8 * ITS steps), so only
+    // the wave holding the end of K ever takes the guarded tail loads.
+    constexpr int kSuper = 8 * ITS;
     int kchunk = (p.K + KW - 1) / KW;
-    kchunk = std::max(8, (kchunk + 7) / 8 * 8);
+    kchunk = std::max(kSuper, (kchunk + kSuper - 1) / kSuper * kSuper);
     const dim3 grid(tiles_m * tiles_n, nbatch);
     const dim3 block(KW * kWave);
     // VA is only used for k-contiguous A (not transposed), VB only for
@@ -537,10 +640,10 @@ hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool 
     va = va && !ta;
     vb = vb && tb;
     const int code = (ta ? 8 : 0) | (tb ? 4 : 0) | (va ? 2 : 0) | (vb ? 1 : 0);
-#define FDL_SPLITK_CASE(C, TA_, TB_, VA_, VB_)                                   \
-    case C:                                                                      \
-        hipLaunchKernelGGL((sgemm_splitk32_kernel<KW, TA_, TB_, VA_, VB_>), grid, \
-                           block, 0, stream, p, tiles_m, tiles_n, kchunk);       \
+#define FDL_SPLITK_CASE(C, TA_, TB_, VA_, VB_)                                          \
+    case C:                                                                             \
+        hipLaunchKernelGGL((sgemm_splitk32_kernel<KW, ITS, TA_, TB_, VA_, VB_>), grid,  \
+                           block, 0, stream, p, tiles_m, tiles_n, kchunk);              \
         break;
     switch (code) {
         FDL_SPLITK_CASE(0, false, false, false, false)
@@ -557,6 +660,15 @@ hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool 
     }
 #undef FDL_SPLITK_CASE
     return hipGetLastError();
+}
+
+// More waves per block for longer K, so each wave's range stays short
+// (about 32-64 steps: one or two super-chunks of loads).
+hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
+                           int nbatch, hipStream_t stream) {
+    if (p.K >= 512) return launch_splitk32_kw<16>(p, ta, tb, va, vb, nbatch, stream);
+    if (p.K >= 128) return launch_splitk32_kw<8>(p, ta, tb, va, vb, nbatch, stream);
+    return launch_splitk32_kw<4>(p, ta, tb, va, vb, nbatch, stream);
 }
 
 template <int MR>
@@ -588,7 +700,10 @@ constexpr int kMaxGridY = 65535;
 // Production tile configurations (BM, BN, BK, WM, WN, PAD, waves per SIMD).
 using CfgTiled128 = TileCfg<128, 128, 16, 64, 64, 4, 1>;
 using CfgTiled64 = TileCfg<64, 64, 16, 32, 32, 4, 1>;
-using CfgTiled256 = TileCfg<256, 256, 16, 128, 64, 4, 1>;
+// Tiled256 reads LDS fragments two k pairs at a time, the next chunk's reads
+// issued ahead of the current chunk's MFMAs (measured +3-4% over whole-tile
+// reads at 4096^3 and 8192^3).
+using CfgTiled256 = TileCfg<256, 256, 16, 128, 64, 4, 1, 0, 2, 0, 1>;
 using CfgTiled256x128 = TileCfg<256, 128, 16, 64, 64, 4, 1>;
 using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
 

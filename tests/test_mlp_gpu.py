@@ -199,6 +199,23 @@ def test_mlp_config2_step(device):
     assert losses[-1] < losses[0]
 
 
+@pytest.mark.parametrize("B,I,H,C", [(300, 50, 20, 10), (64, 30, 17, 40), (1, 8, 4, 3)])
+def test_mlp_step_shapes(device, B, I, H, C):
+    # batch beyond one 256-row chunk of the fused loss kernel, a class count past
+    # its LDS staging limit (separate loss and bias-gradient kernels), batch 1
+    g = rng(B * 7 + C)
+    X = g.random((B, I)).astype(np.float32)
+    labels = g.integers(0, C, B).astype(np.int64)
+    W1 = g.uniform(-np.sqrt(6 / I), np.sqrt(6 / I), (I, H)).astype(np.float32)
+    W2 = g.uniform(-np.sqrt(6 / H), np.sqrt(6 / H), (H, C)).astype(np.float32)
+    b1 = (g.standard_normal(H) * 0.1).astype(np.float32)
+    b2 = (g.standard_normal(C) * 0.1).astype(np.float32)
+    say(f"mlp2 step B={B} I={I} H={H} C={C}")
+    gpu = _step_gpu(X, labels, W1, b1, W2, b2, 0.05)
+    ref = oracle.mlp2_train_step(X, labels, W1, b1, W2, b2, 0.05)
+    _compare_step(gpu, ref)
+
+
 def test_random_fills(device):
     import torch
 
