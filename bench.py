@@ -146,7 +146,15 @@ def mlp_rate(capi, torch, steps=200, warmup=20):
         capi.mlp2_train_step(*args)
 
     ms = time_launches(step, steps, warmup, torch.cuda.current_stream())
-    return 1000.0 / ms, ms, float(buf["loss"].item())
+    loss = float(buf["loss"].item())
+    # The same step captured once into a HIP graph and replayed.
+    handle = capi.mlp2_graph_create(*args)
+    try:
+        gms = time_launches(lambda: capi.mlp2_graph_launch(handle, stream), steps, warmup,
+                            torch.cuda.current_stream())
+    finally:
+        capi.mlp2_graph_destroy(handle)
+    return 1000.0 / ms, ms, loss, 1000.0 / gms, gms
 
 
 def sampled_parity(A, B, C, n, rows=16):
@@ -200,8 +208,9 @@ def sweep(capi, torch, path):
     for n in (777, 1000, 1023):
         launch, *_ = gemm_case(capi, torch, n, n, n, epi=2)
         rec(f"C5b {n}^3 bias+relu", launch, 2.0 * n ** 3, b4(n, n, n, bias=True))
-    sps, ms, _ = mlp_rate(capi, torch)
-    out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps})
+    sps, ms, _, gsps, gms = mlp_rate(capi, torch)
+    out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps,
+                "graph_ms": gms, "graph_steps_per_s": gsps})
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
 
@@ -240,9 +249,13 @@ def main():
 
     mlp = None
     if not args.no_mlp:
-        sps, mlp_ms, loss = mlp_rate(capi, torch)
-        mlp = {"steps_per_s": sps, "ms_per_step": mlp_ms, "final_loss": loss,
-               "config": "784-256-10, batch 256, lr 0.1, fdl_mlp2_train_step (dX included)"}
+        sps, mlp_ms, loss, graph_sps, graph_ms = mlp_rate(capi, torch)
+        mlp = {"steps_per_s": sps, "ms_per_step": mlp_ms,
+               "graph_steps_per_s": graph_sps, "graph_ms_per_step": graph_ms,
+               "final_loss": loss,
+               "config": "784-256-10, batch 256, lr 0.1, full step (forward, softmax-CE, "
+                         "backward incl. dX, SGD): one fdl_mlp2_train_step call (8 kernels) "
+                         "per step; graph = the same step replayed as a HIP graph"}
     if args.sweep:
         sweep(capi, torch, args.sweep)
 

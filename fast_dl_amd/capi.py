@@ -13,10 +13,11 @@ import os
 OP_N, OP_T = 0, 1
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_BIAS_RELU, EPILOGUE_RELU, EPILOGUE_RELU_GRAD = range(5)
 KERNEL_AUTO, KERNEL_TILED128, KERNEL_TILED64, KERNEL_SPLITK32, KERNEL_SKINNY = -1, 0, 1, 2, 3
-KERNEL_TILED256, KERNEL_TILED256X128, KERNEL_TILED128W8 = 4, 5, 6
+KERNEL_TILED256, KERNEL_TILED256X128, KERNEL_TILED128W8, KERNEL_SPLITK16 = 4, 5, 6, 7
 KERNEL_NAMES = {KERNEL_TILED128: "tiled128", KERNEL_TILED64: "tiled64",
                 KERNEL_SPLITK32: "splitk32", KERNEL_SKINNY: "skinny", KERNEL_TILED256: "tiled256",
-                KERNEL_TILED256X128: "tiled256x128", KERNEL_TILED128W8: "tiled128w8"}
+                KERNEL_TILED256X128: "tiled256x128", KERNEL_TILED128W8: "tiled128w8",
+                KERNEL_SPLITK16: "splitk16"}
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _LIB = None
@@ -43,6 +44,11 @@ SIGNATURES = {
     "fdl_sgd_update": (_int, [_vp, _vp, _flt, _i64, _vp]),
     "fdl_mlp2_train_step": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _flt,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fdl_mlp2_graph_create": (_int, [ctypes.POINTER(_vp), _vp, _vp, _i64, _i64, _i64, _i64,
+                                     _vp, _vp, _vp, _vp, _flt, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _vp, _vp]),
+    "fdl_mlp2_graph_launch": (_int, [_vp, _vp]),
+    "fdl_mlp2_graph_destroy": (_int, [_vp]),
     "fdl_fill_uniform": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
     "fdl_fill_normal": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
     "fdl_last_error": (ctypes.c_char_p, []),
@@ -103,6 +109,18 @@ softmax_xent = _checked("fdl_softmax_xent")
 sgd_update = _checked("fdl_sgd_update")
 mlp2_train_step = _checked("fdl_mlp2_train_step")
 fill_uniform = _checked("fdl_fill_uniform")
+mlp2_graph_launch = _checked("fdl_mlp2_graph_launch")
+mlp2_graph_destroy = _checked("fdl_mlp2_graph_destroy")
+
+
+def mlp2_graph_create(*args) -> int:
+    """Capture fdl_mlp2_train_step(*args) into a graph; returns the handle (an int)."""
+    handle = ctypes.c_void_p()
+    lib = load_library()
+    status = lib.fdl_mlp2_graph_create(ctypes.byref(handle), *args)
+    if status != 0:
+        raise FdlError("fdl_mlp2_graph_create", status, lib.fdl_last_error().decode())
+    return handle.value
 fill_normal = _checked("fdl_fill_normal")
 
 

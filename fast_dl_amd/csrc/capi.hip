@@ -36,7 +36,7 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int64_t ldb, int64_t strideB, float* C, int64_t ldc,
                         int64_t strideC, int64_t batch, const float* bias,
                         const float* aux, int epilogue, int kernel, void* stream) {
-    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_TILED128W8) {
+    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_SPLITK16) {
         return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
     }
     if ((transA != FDL_OP_N && transA != FDL_OP_T) ||
@@ -271,6 +271,75 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
     if (st) return st;
     return check_hip(fdl::launch_colsum_sgd(G1, db1, b1, lr, B, Hd, hs),
                      "mlp2_train_step db1 failed");
+}
+
+}  // extern "C"
+
+struct fdl_mlp2_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" {
+
+int fdl_mlp2_graph_create(fdl_mlp2_graph** out, const float* X, const int64_t* labels,
+                          int64_t batch, int64_t in_features, int64_t hidden, int64_t classes,
+                          float* W1, float* b1, float* W2, float* b2, float lr, float* H,
+                          float* logits, float* G2, float* G1, float* dW1, float* db1,
+                          float* dW2, float* db2, float* dX, float* loss, void* stream) {
+    if (!out) return fail(FDL_ERROR_INVALID_VALUE, "mlp2_graph_create: null handle pointer");
+    *out = nullptr;
+    hipStream_t s = as_stream(stream);
+    hipStream_t own = nullptr;
+    if (s == nullptr) {
+        hipError_t e = hipStreamCreateWithFlags(&own, hipStreamNonBlocking);
+        if (e != hipSuccess) return check_hip(e, "mlp2_graph_create: stream");
+        s = own;
+    }
+    auto cleanup = [&] {
+        if (own) (void)hipStreamDestroy(own);
+    };
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        cleanup();
+        return check_hip(e, "mlp2_graph_create: begin capture");
+    }
+    const int st = fdl_mlp2_train_step(X, labels, batch, in_features, hidden, classes, W1, b1,
+                                       W2, b2, lr, H, logits, G2, G1, dW1, db1, dW2, db2, dX,
+                                       loss, s);
+    hipGraph_t graph = nullptr;
+    e = hipStreamEndCapture(s, &graph);
+    if (st != FDL_SUCCESS || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        cleanup();
+        return st != FDL_SUCCESS ? st : check_hip(e, "mlp2_graph_create: end capture");
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    cleanup();
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return check_hip(e, "mlp2_graph_create: instantiate");
+    }
+    auto* g = new fdl_mlp2_graph;
+    g->graph = graph;
+    g->exec = exec;
+    *out = g;
+    return FDL_SUCCESS;
+}
+
+int fdl_mlp2_graph_launch(fdl_mlp2_graph* g, void* stream) {
+    if (!g || !g->exec) return fail(FDL_ERROR_INVALID_VALUE, "mlp2_graph_launch: null graph");
+    return check_hip(hipGraphLaunch(g->exec, as_stream(stream)), "mlp2_graph_launch failed");
+}
+
+int fdl_mlp2_graph_destroy(fdl_mlp2_graph* g) {
+    if (!g) return FDL_SUCCESS;
+    hipError_t e1 = g->exec ? hipGraphExecDestroy(g->exec) : hipSuccess;
+    hipError_t e2 = g->graph ? hipGraphDestroy(g->graph) : hipSuccess;
+    delete g;
+    if (e1 != hipSuccess) return check_hip(e1, "mlp2_graph_destroy");
+    return check_hip(e2, "mlp2_graph_destroy");
 }
 
 int fdl_fill_uniform(float* data, int64_t n, float low, float high, uint64_t seed,

@@ -47,6 +47,7 @@ enum class GemmKernel : int {
     Tiled256 = 4,     // 256x256x16 tile, 8 waves of 128x64
     Tiled256x128 = 5, // 256x128x16 tile, 8 waves of 64x64
     Tiled128W8 = 6,   // 128x128x16 tile, 8 waves of 32x64
+    SplitK16 = 7,     // 16x16 output tile (16x16x4 MFMA), K split over waves
     Auto = -1,
 };
 

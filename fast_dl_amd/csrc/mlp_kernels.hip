@@ -173,7 +173,13 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
     const int t = threadIdx.x;
     const float inv_b = 1.0f / (float)batch;
     float lsum = 0.0f;
-    float dbc = 0.0f;  // running column sum for class t (t < classes)
+    // Column sums of the gradient: thread t adds class cls over the rows
+    // r = grp, grp + ngrp, ... of each chunk (ngrp groups of cpad threads).
+    const int cpad = classes <= 8 ? 8 : (classes <= 16 ? 16 : 32);
+    const int ngrp = kBlock / cpad;
+    const int cls = t % cpad;
+    const int grp = t / cpad;
+    float dbc = 0.0f;
     for (int64_t r0 = 0; r0 < batch; r0 += kBlock) {
         const int rows = (int)min<int64_t>(kBlock, batch - r0);
         const int n = rows * (int)classes;
@@ -199,16 +205,22 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
         __syncthreads();
         float* gdst = grad + r0 * classes;
         for (int e = t; e < n; e += kBlock) gdst[e] = zs[e];
-        if (t < classes) {
-            for (int r = 0; r < rows; ++r) dbc += zs[r * classes + t];
+        if (cls < classes) {
+            for (int r = grp; r < rows; r += ngrp) dbc += zs[r * classes + cls];
         }
         __syncthreads();
     }
+    // Group partials of each class, added in group order.
+    part[t] = dbc;
+    __syncthreads();
     if (t < classes) {
-        db[t] = dbc;
-        const float step = lr * dbc;
+        float d = part[t];
+        for (int g = 1; g < ngrp; ++g) d += part[g * cpad + t];
+        db[t] = d;
+        const float step = lr * d;
         bparam[t] = bparam[t] - step;
     }
+    __syncthreads();
     part[t] = lsum;
     __syncthreads();
     for (int w = kBlock / 2; w > 0; w >>= 1) {

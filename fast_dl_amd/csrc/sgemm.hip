@@ -491,6 +491,109 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 }
 
 // ---------------------------------------------------------------------------
+// Small-problem kernel with 16x16 output tiles (v_mfma_f32_16x16x4_f32), for
+// outputs too small to give 32x32 tiles to every CU.  Lane layout:
+//   operand a: lane l supplies A[i = l % 16][kk = l / 16]
+//   operand b: lane l supplies B[kk = l / 16][j = l % 16]
+//   result   : lane l, register r holds D[4 * (l / 16) + r][l % 16]
+// A group covers 16 reduction steps: at step s (0..3) the lane in quarter q
+// supplies k = k0 + 4q + s (the same permutation for A and B), so a lane's
+// four A values are contiguous.  K is split over KW waves; groups are loaded
+// ITS at a time into two alternating register buffers; partials meet in LDS.
+// ---------------------------------------------------------------------------
+template <bool TA, bool TB, bool VA, bool VB>
+__device__ __forceinline__ void splitk16_load_group(const float* __restrict__ A,
+                                                    const float* __restrict__ B,
+                                                    const GemmParams& p, int row, int col,
+                                                    int kb, int kend, bool tail, float a[4],
+                                                    float b[4]) {
+    // Same contract as splitk_load_group: row/col are clamped into the matrix.
+    splitk_load_group<TA, TB, VA, VB>(A, B, p, row, col, kb, kend, tail, a, b);
+}
+
+template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(KW * 64)
+sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
+    __shared__ float red[KW][4][kWave];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int i = lane & 15;
+    const int q = lane >> 4;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * 16;
+    const int n0 = tn * 16;
+    const int64_t bz = blockIdx.y;
+    const float* __restrict__ A = p.A + bz * p.strideA;
+    const float* __restrict__ B = p.B + bz * p.strideB;
+
+    const int row = min(m0 + i, p.M - 1);
+    const int col = min(n0 + i, p.N - 1);
+    const int kbeg = wave * kchunk;
+    const int kend = min(p.K, kbeg + kchunk);
+    const int groups = kend > kbeg ? (kend - kbeg + 15) / 16 : 0;
+    const int supers = (groups + ITS - 1) / ITS;
+
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float a0[ITS][4], b0[ITS][4], a1[ITS][4], b1[ITS][4];
+    auto load_super = [&](int sc, float (&a)[ITS][4], float (&b)[ITS][4]) {
+        const int k0 = kbeg + 16 * sc * ITS;
+        if (k0 + 16 * ITS <= kend) {
+#pragma unroll
+            for (int g = 0; g < ITS; ++g)
+                splitk16_load_group<TA, TB, VA, VB>(A, B, p, row, col, k0 + 16 * g + 4 * q, kend,
+                                                    false, a[g], b[g]);
+        } else {
+#pragma unroll
+            for (int g = 0; g < ITS; ++g)
+                splitk16_load_group<TA, TB, VA, VB>(A, B, p, row, col, k0 + 16 * g + 4 * q, kend,
+                                                    true, a[g], b[g]);
+        }
+    };
+    auto mfma_super = [&](const float (&a)[ITS][4], const float (&b)[ITS][4]) {
+#pragma unroll
+        for (int g = 0; g < ITS; ++g)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][s], b[g][s], acc, 0, 0, 0);
+    };
+
+    if (supers > 0) load_super(0, a0, b0);
+    for (int sc = 0; sc < supers; sc += 2) {
+        if (sc + 1 < supers) load_super(sc + 1, a1, b1);
+        mfma_super(a0, b0);
+        if (sc + 1 < supers) {
+            if (sc + 2 < supers) load_super(sc + 2, a0, b0);
+            mfma_super(a1, b1);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+
+    float* __restrict__ C = p.C + bz * p.strideC;
+    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+    for (int e = tid; e < 4 * kWave; e += KW * kWave) {
+        const int r = e / kWave;
+        const int ln = e % kWave;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) v += red[w][r][ln];
+        const int gi = m0 + 4 * (ln >> 4) + r;
+        const int gj = n0 + (ln & 15);
+        if (gi < p.M && gj < p.N) {
+            const int64_t off = (int64_t)gi * p.ldc + gj;
+            store_epilogue(v, p, C, aux, upd, off, gj);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny kernel for M <= MR (MR <= 8) with B not transposed: a bandwidth
 // kernel whose cost is one pass over B.  A block owns a strip of 16 columns
 // and the whole K range: CL lanes across the strip (4 lanes x float4 when VB,
@@ -622,10 +725,9 @@ hipError_t launch_tiled(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
     return hipGetLastError();
 }
 
-template <int KW>
+template <int KW, int ITS = 4>
 hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                               int nbatch, hipStream_t stream) {
-    constexpr int ITS = 4;
     const int tiles_m = (p.M + 31) / 32;
     const int tiles_n = (p.N + 31) / 32;
     // K range per wave, a multiple of one super-chunk (8 * ITS steps), so only
@@ -662,13 +764,57 @@ hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
     return hipGetLastError();
 }
 
+template <int KW, int ITS = 1>
+hipError_t launch_splitk16_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
+                              int nbatch, hipStream_t stream) {
+    const int tiles_m = (p.M + 15) / 16;
+    const int tiles_n = (p.N + 15) / 16;
+    constexpr int kSuper = 16 * ITS;
+    int kchunk = (p.K + KW - 1) / KW;
+    kchunk = std::max(kSuper, (kchunk + kSuper - 1) / kSuper * kSuper);
+    const dim3 grid(tiles_m * tiles_n, nbatch);
+    const dim3 block(KW * kWave);
+    va = va && !ta;
+    vb = vb && tb;
+    const int code = (ta ? 8 : 0) | (tb ? 4 : 0) | (va ? 2 : 0) | (vb ? 1 : 0);
+#define FDL_SPLITK16_CASE(C, TA_, TB_, VA_, VB_)                                        \
+    case C:                                                                             \
+        hipLaunchKernelGGL((sgemm_splitk16_kernel<KW, ITS, TA_, TB_, VA_, VB_>), grid,  \
+                           block, 0, stream, p, tiles_m, tiles_n, kchunk);              \
+        break;
+    switch (code) {
+        FDL_SPLITK16_CASE(0, false, false, false, false)
+        FDL_SPLITK16_CASE(2, false, false, true, false)
+        FDL_SPLITK16_CASE(4, false, true, false, false)
+        FDL_SPLITK16_CASE(5, false, true, false, true)
+        FDL_SPLITK16_CASE(6, false, true, true, false)
+        FDL_SPLITK16_CASE(7, false, true, true, true)
+        FDL_SPLITK16_CASE(8, true, false, false, false)
+        FDL_SPLITK16_CASE(12, true, true, false, false)
+        FDL_SPLITK16_CASE(13, true, true, false, true)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef FDL_SPLITK16_CASE
+    return hipGetLastError();
+}
+
+// Waves per block by K (measured on the MLP-step shapes: 16 waves from
+// K = 512, 8 from 128, else 4; one group in flight per buffer).
+hipError_t launch_splitk16(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
+                           int nbatch, hipStream_t stream) {
+    if (p.K >= 512) return launch_splitk16_kw<16, 1>(p, ta, tb, va, vb, nbatch, stream);
+    if (p.K >= 128) return launch_splitk16_kw<8, 1>(p, ta, tb, va, vb, nbatch, stream);
+    return launch_splitk16_kw<4, 1>(p, ta, tb, va, vb, nbatch, stream);
+}
+
 // More waves per block for longer K, so each wave's range stays short
 // (about 32-64 steps: one or two super-chunks of loads).
 hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                            int nbatch, hipStream_t stream) {
-    if (p.K >= 512) return launch_splitk32_kw<16>(p, ta, tb, va, vb, nbatch, stream);
-    if (p.K >= 128) return launch_splitk32_kw<8>(p, ta, tb, va, vb, nbatch, stream);
-    return launch_splitk32_kw<4>(p, ta, tb, va, vb, nbatch, stream);
+    if (p.K >= 512) return launch_splitk32_kw<16, 2>(p, ta, tb, va, vb, nbatch, stream);
+    if (p.K >= 128) return launch_splitk32_kw<8, 2>(p, ta, tb, va, vb, nbatch, stream);
+    return launch_splitk32_kw<4, 2>(p, ta, tb, va, vb, nbatch, stream);
 }
 
 template <int MR>
@@ -754,6 +900,7 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::Tiled256: return "tiled256";
         case GemmKernel::Tiled256x128: return "tiled256x128";
         case GemmKernel::Tiled128W8: return "tiled128w8";
+        case GemmKernel::SplitK16: return "splitk16";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -768,8 +915,12 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     const int64_t t64 = (int64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
     constexpr int64_t kCUs = 256;
     // Too few 64x64 tiles to occupy the GPU, or too short a K loop to
-    // amortise LDS staging: split K over the waves of a block instead.
-    if (t64 < kCUs || p.K < 64) return GemmKernel::SplitK32;
+    // amortise LDS staging: split K over the waves of a block instead, with
+    // 16x16 output tiles when 32x32 ones would leave most CUs idle.
+    if (t64 < kCUs || p.K < 64) {
+        const int64_t t32 = (int64_t)((p.M + 31) / 32) * ((p.N + 31) / 32) * batch;
+        return t32 < 128 ? GemmKernel::SplitK16 : GemmKernel::SplitK32;
+    }
     GemmKernel best = GemmKernel::Tiled64;
     double best_time = 0.0;
     bool first = true;
@@ -819,6 +970,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::SplitK32:
                 err = launch_splitk32(p, transA, transB, va, vb, nb, stream);
+                break;
+            case GemmKernel::SplitK16:
+                err = launch_splitk16(p, transA, transB, va, vb, nb, stream);
                 break;
             case GemmKernel::Skinny:
                 err = launch_skinny(p, transA, vb, nb, stream);

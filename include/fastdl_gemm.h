@@ -7,9 +7,10 @@
  * the device's null stream, which is what the reference's implicit
  * legacy-default-stream launches used.
  *
- * No entry point allocates device or host memory, none throws, and all are
- * asynchronous with respect to the host: they only validate arguments and
- * enqueue kernels.  A non-zero return is one of the negative fdl_status
+ * No entry point allocates device memory and none throws.  All but the
+ * graph create/destroy pair (which build host-side HIP graph objects) allocate
+ * no host memory either, and all others are asynchronous with respect to the
+ * host: they only validate arguments and enqueue kernels.  A non-zero return is one of the negative fdl_status
  * codes; fdl_last_error() returns a message for the last failure on the
  * calling thread.
  *
@@ -93,7 +94,8 @@ typedef enum fdl_kernel {
     FDL_KERNEL_SKINNY = 3,     /* VALU strip kernel, M <= 8 and transB == N         */
     FDL_KERNEL_TILED256 = 4,   /* 256x256x16 LDS double-buffered MFMA tile, 8 waves */
     FDL_KERNEL_TILED256X128 = 5, /* 256x128x16 tile, 8 waves                        */
-    FDL_KERNEL_TILED128W8 = 6  /* 128x128x16 tile, 8 waves of 32x64                 */
+    FDL_KERNEL_TILED128W8 = 6, /* 128x128x16 tile, 8 waves of 32x64                 */
+    FDL_KERNEL_SPLITK16 = 7    /* 16x16 tile (16x16x4 MFMA), K split over waves     */
 } fdl_kernel;
 
 /*
@@ -207,6 +209,29 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels,
                         float* H, float* logits, float* G2, float* G1,
                         float* dW1, float* db1, float* dW2, float* db2,
                         float* dX, float* loss, void* stream);
+
+/*
+ * The same training step captured once into a HIP graph and replayed: one
+ * launch per step instead of eight, for loops that keep the same buffers
+ * (refill X and labels in place between steps).  create captures
+ * fdl_mlp2_train_step with these exact pointers on `stream` (a temporary
+ * stream when NULL) and instantiates it; launch replays it on `stream`;
+ * destroy releases the graph.  Nothing runs at create time.  No reference
+ * counterpart (the reference has no training step on the GPU); this is the
+ * host-launch side of the step's runtime.
+ */
+typedef struct fdl_mlp2_graph fdl_mlp2_graph;
+
+int fdl_mlp2_graph_create(fdl_mlp2_graph** graph,
+                          const float* X, const int64_t* labels,
+                          int64_t batch, int64_t in_features,
+                          int64_t hidden, int64_t classes,
+                          float* W1, float* b1, float* W2, float* b2, float lr,
+                          float* H, float* logits, float* G2, float* G1,
+                          float* dW1, float* db1, float* dW2, float* db2,
+                          float* dX, float* loss, void* stream);
+int fdl_mlp2_graph_launch(fdl_mlp2_graph* graph, void* stream);
+int fdl_mlp2_graph_destroy(fdl_mlp2_graph* graph);
 
 /*
  * Fill with uniform values in (low, high] or normal values, from a

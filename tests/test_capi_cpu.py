@@ -82,7 +82,7 @@ def test_kernel_choice():
     assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED256
     assert capi.kernel_choice(0, 0, 8, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 8, 4096, 4096) != capi.KERNEL_SKINNY
-    assert capi.kernel_choice(0, 0, 256, 128, 784) == capi.KERNEL_SPLITK32
+    assert capi.kernel_choice(0, 0, 256, 128, 784) == capi.KERNEL_SPLITK16
 
 
 def test_golden_fixtures_reproduced_by_oracle():

@@ -18,7 +18,8 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, say, stream
 pytestmark = pytest.mark.gpu
 
 FAMILIES = [capi.KERNEL_TILED128, capi.KERNEL_TILED64, capi.KERNEL_SPLITK32,
-            capi.KERNEL_TILED256, capi.KERNEL_TILED256X128, capi.KERNEL_TILED128W8]
+            capi.KERNEL_TILED256, capi.KERNEL_TILED256X128, capi.KERNEL_TILED128W8,
+            capi.KERNEL_SPLITK16]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 
 

@@ -216,6 +216,55 @@ def test_mlp_step_shapes(device, B, I, H, C):
     _compare_step(gpu, ref)
 
 
+def _alloc_step(X, labels, W1, b1, W2, b2):
+    import torch
+
+    B, I = X.shape
+    Hd, Cc = W1.shape[1], W2.shape[1]
+    t = {k: dev(v.copy()) for k, v in dict(X=X, labels=labels, W1=W1, b1=b1, W2=W2, b2=b2).items()}
+    for name, shape in dict(H=(B, Hd), logits=(B, Cc), G2=(B, Cc), G1=(B, Hd), dW1=(I, Hd),
+                            db1=(Hd,), dW2=(Hd, Cc), db2=(Cc,), dX=(B, I), loss=(1,)).items():
+        t[name] = torch.full(shape, float("nan"), device="cuda")
+    p = {k: v.data_ptr() for k, v in t.items()}
+    args = (p["X"], p["labels"], B, I, Hd, Cc, p["W1"], p["b1"], p["W2"], p["b2"], 0.1, p["H"],
+            p["logits"], p["G2"], p["G1"], p["dW1"], p["db1"], p["dW2"], p["db2"], p["dX"],
+            p["loss"])
+    return t, args
+
+
+def test_mlp_graph_replays_match_eager(device):
+    # Every replay of the captured step must equal the eager step exactly (all
+    # kernels are deterministic), with eager work and synchronisations between
+    # the replays.
+    import torch
+
+    g = rng(77)
+    B, I, H, C = 256, 784, 256, 10
+    X = g.random((B, I)).astype(np.float32)
+    labels = g.integers(0, C, B).astype(np.int64)
+    W1 = g.uniform(-np.sqrt(6 / I), np.sqrt(6 / I), (I, H)).astype(np.float32)
+    W2 = g.uniform(-np.sqrt(6 / H), np.sqrt(6 / H), (H, C)).astype(np.float32)
+    b1 = np.zeros(H, np.float32)
+    b2 = np.zeros(C, np.float32)
+    te, eargs = _alloc_step(X, labels, W1, b1, W2, b2)
+    tg, gargs = _alloc_step(X, labels, W1, b1, W2, b2)
+    s = stream()
+    say("mlp2 graph create")
+    handle = capi.mlp2_graph_create(*gargs, s)
+    try:
+        for step in range(5):
+            say(f"mlp2 graph replay {step}")
+            capi.mlp2_train_step(*eargs, s)
+            capi.mlp2_graph_launch(handle, s)
+            torch.cuda.synchronize()
+            junk = torch.randn(1000, device="cuda").sum().item()  # unrelated eager work
+            assert np.isfinite(junk)
+            for k in ("W1", "b1", "W2", "b2", "loss", "dX", "G1", "dW1", "db1"):
+                assert torch.equal(te[k], tg[k]), f"replay {step}: {k} differs"
+    finally:
+        capi.mlp2_graph_destroy(handle)
+
+
 def test_random_fills(device):
     import torch
 
