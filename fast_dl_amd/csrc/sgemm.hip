@@ -595,18 +595,18 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 
 // ---------------------------------------------------------------------------
 // Skinny kernel for M <= MR (MR <= 8) with B not transposed: a bandwidth
-// kernel whose cost is one pass over B.  A block owns a strip of 16 columns
-// and the whole K range: CL lanes across the strip (4 lanes x float4 when VB,
-// else 16 lanes x 1) and KL = 256 / CL lanes along K.  Each lane keeps MR x CW
-// partial sums in registers; the KL partials meet in LDS and are added in
-// lane order.  Strips are renumbered so the 8 XCDs each stream one
-// contiguous band of B's columns (neighbouring strips share 128-byte lines).
+// kernel whose cost is one pass over B.  A block of NT threads owns a strip of
+// STRIP columns and the whole K range: CL lanes across the strip (float4 each
+// when VB) and KL = NT / CL lanes along K.  Each lane issues UNR rows of B
+// before using any (UNR independent 16-byte loads in flight per lane), keeps
+// MR x CW partial sums in registers, and the KL partials meet in LDS, added in
+// lane order.  Strips are renumbered so the 8 XCDs each stream one contiguous
+// band of B's columns.  Column and row indices are clamped into the matrices:
+// lanes past the edge load valid data that only reaches outputs never stored.
 // ---------------------------------------------------------------------------
-template <int MR, bool TA, bool VB>
-__global__ void __launch_bounds__(256)
+template <int MR, bool TA, bool VB, int STRIP, int NT, int UNR>
+__global__ void __launch_bounds__(NT)
 sgemm_skinny_kernel(GemmParams p, int strips) {
-    constexpr int NT = 256;
-    constexpr int STRIP = 16;
     constexpr int CW = VB ? 4 : 1;
     constexpr int CL = STRIP / CW;
     constexpr int KL = NT / CL;
@@ -618,11 +618,13 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
 
     int sid = blockIdx.x;
     if ((strips & 7) == 0) sid = (sid & 7) * (strips >> 3) + (sid >> 3);
-    const int n0 = sid * STRIP + cl * CW;
     const int64_t bz = blockIdx.y;
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
-    const bool col_ok = n0 < p.N;  // VB: N % 4 == 0, so the float4 is whole
+    // VB: N % 4 == 0, so clamping to the last float4 keeps whole vectors.
+    const int n0 = min(sid * STRIP + cl * CW, p.N - CW);
+    const int M = p.M;
+    const int K = p.K;
 
     float acc[MR][CW];
 #pragma unroll
@@ -630,22 +632,43 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
 #pragma unroll
         for (int c = 0; c < CW; ++c) acc[m][c] = 0.0f;
 
-    const int M = p.M;
-#pragma unroll 4
-    for (int k = kl; k < p.K; k += KL) {
-        float b[CW];
+    auto a_at = [&](int m, int k) {
+        const int mm = min(m, M - 1);
+        return TA ? A[(int64_t)k * p.lda + mm] : A[(int64_t)mm * p.lda + k];
+    };
+    auto b_at = [&](int k, float (&b)[CW]) {
         if (VB) {
-            floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (col_ok) v = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + n0);
+            const floatx4 v = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + n0);
 #pragma unroll
             for (int c = 0; c < CW; ++c) b[c] = v[c];
         } else {
-            b[0] = col_ok ? B[(int64_t)k * p.ldb + n0] : 0.0f;
+            b[0] = B[(int64_t)k * p.ldb + n0];
         }
+    };
+
+    int k = kl;
+    for (; k + (UNR - 1) * KL < K; k += UNR * KL) {
+        float b[UNR][CW];
+        float a[UNR][MR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) b_at(k + u * KL, b[u]);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) a[u][m] = a_at(m, k + u * KL);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int c = 0; c < CW; ++c) acc[m][c] = fmaf(a[u][m], b[u][c], acc[m][c]);
+    }
+    for (; k < K; k += KL) {
+        float b[CW];
+        b_at(k, b);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            float a = 0.0f;
-            if (m < M) a = TA ? A[(int64_t)k * p.lda + m] : A[(int64_t)m * p.lda + k];
+            const float a = a_at(m, k);
 #pragma unroll
             for (int c = 0; c < CW; ++c) acc[m][c] = fmaf(a, b[c], acc[m][c]);
         }
@@ -817,20 +840,29 @@ hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool 
     return launch_splitk32_kw<4, 2>(p, ta, tb, va, vb, nbatch, stream);
 }
 
+template <int MR, int STRIP, int NT, int UNR>
+hipError_t launch_skinny_cfg(const GemmParams& p, bool ta, bool vb, int nbatch,
+                             hipStream_t stream) {
+    const int strips = (p.N + STRIP - 1) / STRIP;
+    const dim3 grid(strips, nbatch);
+    const dim3 block(NT);
+    if (ta) {
+        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, true, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, false, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+    } else {
+        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, true, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, false, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+    }
+    return hipGetLastError();
+}
+
+// 16-column strips, 256 threads; 8 B rows in flight per lane for M == 1,
+// 512 threads with 8 rows in flight for larger M (measured on K = N = 4096).
 template <int MR>
 hipError_t launch_skinny_mr(const GemmParams& p, bool ta, bool vb, int nbatch,
                             hipStream_t stream) {
-    const int strips = (p.N + 15) / 16;
-    const dim3 grid(strips, nbatch);
-    const dim3 block(256);
-    if (ta) {
-        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, true>), grid, block, 0, stream, p, strips);
-        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, false>), grid, block, 0, stream, p, strips);
-    } else {
-        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, true>), grid, block, 0, stream, p, strips);
-        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, false>), grid, block, 0, stream, p, strips);
-    }
-    return hipGetLastError();
+    if (MR == 1) return launch_skinny_cfg<MR, 16, 256, 8>(p, ta, vb, nbatch, stream);
+    return launch_skinny_cfg<MR, 16, 512, 8>(p, ta, vb, nbatch, stream);
 }
 
 hipError_t launch_skinny(const GemmParams& p, bool ta, bool vb, int nbatch,
