@@ -72,6 +72,57 @@ def time_launches(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per launch
 
 
+def launch_percentiles(fn, steps, stream):
+    """Per-launch durations from events recorded between back-to-back launches on
+    ``stream``: (median, p10, p90) in ms.  Each event pair brackets one launch."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for i in range(steps):
+        fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    d = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    pick = lambda q: d[min(len(d) - 1, int(q * len(d)))]  # noqa: E731
+    return pick(0.5), pick(0.1), pick(0.9)
+
+
+def vendor_case(torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1):
+    """The same GEMM through PyTorch (rocBLAS / hipBLASLt, full fp32), for comparison only.
+
+    Bias+ReLU is ``addmm`` followed by an in-place ``relu_`` (two launches), which
+    is how a caller without a fused epilogue would write it.
+    """
+    torch.backends.cuda.matmul.allow_tf32 = False
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    a_shape = (batch, K, M) if ta else (batch, M, K)
+    b_shape = (batch, N, K) if tb else (batch, K, N)
+    As = [torch.randn(a_shape, generator=gen, device="cuda") for _ in range(rotate)]
+    Bs = [torch.randn(b_shape, generator=gen, device="cuda") for _ in range(rotate)]
+    Cs = [torch.empty((batch, M, N), device="cuda") for _ in range(rotate)]
+    bias = torch.randn((N,), generator=gen, device="cuda") * 0.1
+    state = {"i": 0}
+
+    def launch():
+        i = state["i"]
+        state["i"] = (i + 1) % rotate
+        a = As[i].transpose(1, 2) if ta else As[i]
+        b = Bs[i].transpose(1, 2) if tb else Bs[i]
+        if batch == 1:
+            if epi in (1, 2):
+                torch.addmm(bias, a[0], b[0], out=Cs[i][0])
+            else:
+                torch.mm(a[0], b[0], out=Cs[i][0])
+        else:
+            torch.bmm(a, b, out=Cs[i])
+        if epi == 2:
+            Cs[i].relu_()
+
+    return launch
+
+
 def gemm_case(capi, torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1):
     """Resident operands and a launcher closure for one GEMM configuration.
 
@@ -100,8 +151,24 @@ def gemm_case(capi, torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1
     return launch, As[0], Bs[0], Cs[0]
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(n, rows):
-    """Restated reference CPU loop (oracle/gemm_cpu, 1 thread) on a row block."""
+    """Restated reference CPU loop (oracle/gemm_cpu, 1 thread) on a row block.
+
+    The reference has no threading, so the loop runs on one core; the process
+    is pinned to a single CPU for the timed call and unpinned afterwards.  The
+    loop's cost per row is uniform, so the rate of a row block is the rate of
+    the whole product.
+    """
     import numpy as np
 
     import oracle
@@ -109,17 +176,24 @@ def cpu_baseline(n, rows):
     g = np.random.default_rng(0)
     A = g.standard_normal((rows, n)).astype(np.float32)
     B = g.standard_normal((n, n)).astype(np.float32)
-    t0 = time.perf_counter()
-    oracle.gemm_cpu(A, B)
-    dt = time.perf_counter() - t0
+    saved = os.sched_getaffinity(0)
+    core = min(saved)
+    os.sched_setaffinity(0, {core})
+    try:
+        t0 = time.perf_counter()
+        oracle.gemm_cpu(A, B)
+        dt = time.perf_counter() - t0
+    finally:
+        os.sched_setaffinity(0, saved)
     flops = 2.0 * rows * n * n
     return {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{rows} of {n} rows of the {n}^3 NN GEMM (gemm_cpu loop, gcc -O2, 1 thread), "
-                  f"{dt:.2f} s",
+        "sample": f"{rows} of {n} rows of the {n}^3 NN GEMM (gemm_cpu loop, gcc -O2 "
+                  f"-ffp-contract=off, 1 thread pinned to cpu {core}), {dt:.2f} s; host "
+                  f"{cpu_model()}, {len(saved)} cpus visible",
     }
 
 
@@ -173,11 +247,36 @@ def sampled_parity(A, B, C, n, rows=16):
     return bool(np.all(np.abs(c - ref) <= bound))
 
 
+def torch_mlp_rate(torch, steps=200, warmup=20):
+    """The same 784-256-10 step written in eager PyTorch (autograd, fused
+    cross_entropy, torch.optim.SGD), for comparison only: steps/s."""
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    B, I, H, C = 256, 784, 256, 10
+    X = torch.rand((B, I), generator=gen, device="cuda")
+    labels = torch.randint(0, C, (B,), generator=gen, device="cuda", dtype=torch.int64)
+    W1 = ((torch.rand((I, H), generator=gen, device="cuda") * 2 - 1) * (6 / I) ** 0.5)
+    W2 = ((torch.rand((H, C), generator=gen, device="cuda") * 2 - 1) * (6 / H) ** 0.5)
+    params = [W1.requires_grad_(), torch.zeros(H, device="cuda", requires_grad=True),
+              W2.requires_grad_(), torch.zeros(C, device="cuda", requires_grad=True)]
+    opt = torch.optim.SGD(params, lr=0.1)
+
+    def step():
+        opt.zero_grad(set_to_none=False)
+        h = torch.relu(torch.addmm(params[1], X, params[0]))
+        loss = torch.nn.functional.cross_entropy(torch.addmm(params[3], h, params[2]), labels)
+        loss.backward()
+        opt.step()
+
+    ms = time_launches(step, steps, warmup, torch.cuda.current_stream())
+    return 1000.0 / ms, ms
+
+
 def sweep(capi, torch, path):
-    """Every BASELINE configuration, one line each (for DESIGN.md / profiles)."""
+    """Every BASELINE configuration, one line each, with the same GEMM through
+    PyTorch's vendor BLAS (``vendor_ms``) timed the same way beside it."""
     out = []
 
-    def rec(name, launch, flops, nbytes, steps=30, warmup=5):
+    def rec(name, launch, vendor, flops, nbytes, steps=30, warmup=5):
         ms = time_launches(launch, steps, warmup, torch.cuda.current_stream())
         t = ms / 1e3
         ridge = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
@@ -186,31 +285,39 @@ def sweep(capi, torch, path):
                "bound": bound,
                "frac": (flops / t / 1e12 / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma"
                else (nbytes / t / 1e9 / PEAK_HBM_GBS)}
+        if vendor is not None:
+            row["vendor_ms"] = time_launches(vendor, steps, warmup, torch.cuda.current_stream())
+            row["speedup_vs_vendor"] = row["vendor_ms"] / ms
         out.append(row)
         print(json.dumps(row), file=sys.stderr, flush=True)
 
     def b4(M, N, K, batch=1, bias=False):
         return 4.0 * batch * (M * K + K * N + M * N) + (4.0 * N if bias else 0.0)
 
-    launch, *_ = gemm_case(capi, torch, 256, 128, 784)
-    rec("C1 256x128x784 NN", launch, 2.0 * 256 * 128 * 784, b4(256, 128, 784))
+    def both(M, N, K, **kw):
+        launch, *_ = gemm_case(capi, torch, M, N, K, **kw)
+        return launch, vendor_case(torch, M, N, K, **kw)
+
+    rec("C1 256x128x784 NN", *both(256, 128, 784), 2.0 * 256 * 128 * 784, b4(256, 128, 784))
     for n in (1024, 2048, 4096, 8192):
-        launch, *_ = gemm_case(capi, torch, n, n, n)
-        rec(f"C3 {n}^3 NN", launch, 2.0 * n ** 3, b4(n, n, n), steps=10 if n == 8192 else 30)
+        rec(f"C3 {n}^3 NN", *both(n, n, n), 2.0 * n ** 3, b4(n, n, n),
+            steps=10 if n == 8192 else 30)
     for tb in (0, 1):
-        launch, *_ = gemm_case(capi, torch, 128, 128, 64, tb=tb, batch=64, rotate=40)
-        rec(f"C4 64x(128x128x64) {'NT' if tb else 'NN'}", launch, 2.0 * 64 * 128 * 128 * 64,
+        rec(f"C4 64x(128x128x64) {'NT' if tb else 'NN'}",
+            *both(128, 128, 64, tb=tb, batch=64, rotate=40), 2.0 * 64 * 128 * 128 * 64,
             b4(128, 128, 64, 64))
     for m in (1, 8):
-        launch, *_ = gemm_case(capi, torch, m, 4096, 4096, epi=2, rotate=6)
-        rec(f"C5a M={m} K=N=4096 bias+relu", launch, 2.0 * m * 4096 * 4096,
-            b4(m, 4096, 4096, bias=True))
+        rec(f"C5a M={m} K=N=4096 bias+relu", *both(m, 4096, 4096, epi=2, rotate=6),
+            2.0 * m * 4096 * 4096, b4(m, 4096, 4096, bias=True))
     for n in (777, 1000, 1023):
-        launch, *_ = gemm_case(capi, torch, n, n, n, epi=2)
-        rec(f"C5b {n}^3 bias+relu", launch, 2.0 * n ** 3, b4(n, n, n, bias=True))
+        rec(f"C5b {n}^3 bias+relu", *both(n, n, n, epi=2), 2.0 * n ** 3,
+            b4(n, n, n, bias=True))
     sps, ms, _, gsps, gms = mlp_rate(capi, torch)
+    tsps, tms = torch_mlp_rate(torch)
     out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps,
-                "graph_ms": gms, "graph_steps_per_s": gsps})
+                "graph_ms": gms, "graph_steps_per_s": gsps, "torch_eager_ms": tms,
+                "torch_eager_steps_per_s": tsps})
+    print(json.dumps(out[-1]), file=sys.stderr, flush=True)
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
 
@@ -245,6 +352,8 @@ def main():
         return
     flops = 2.0 * n * n * n
     tflops = flops / (ms / 1e3) / 1e12
+    med, p10, p90 = launch_percentiles(launch, args.steps, stream)
+    vendor_ms = time_launches(vendor_case(torch, n, n, n), max(10, args.steps // 5), 3, stream)
     parity = sampled_parity(A, B, C, n)
 
     mlp = None
@@ -261,9 +370,13 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(n, rows=32)
+        cpu = cpu_baseline(n, rows=64)
 
-    kernel = capi.KERNEL_NAMES.get(capi.kernel_choice(0, 0, n, n, n), "auto")
+    family = capi.kernel_choice(0, 0, n, n, n)
+    kernel = capi.KERNEL_NAMES.get(family, "auto")
+    kernel_fn = {capi.KERNEL_DMA256: "sgemm_dma_kernel", capi.KERNEL_SKINNY: "sgemm_skinny_kernel",
+                 capi.KERNEL_SPLITK32: "sgemm_splitk32_kernel",
+                 capi.KERNEL_SPLITK16: "sgemm_splitk16_kernel"}.get(family, "sgemm_tiled_kernel")
     line = {
         "metric": "fp32 GEMM TFLOP/s at M=N=K=4096 (% MI355X fp32 peak); MLP train steps/s",
         "value": tflops,
@@ -272,19 +385,22 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "launch_ms": {"median": med, "p10": p10, "p90": p90},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (torch.randn on device, seed 0)",
         "config": {"workload": f"sgemm NN row-major M=N=K={n}, A,B ~ N(0,1)",
-                   "kernel": f"sgemm_tiled_kernel ({kernel})", "parallelism": "single GPU"},
+                   "kernel": f"{kernel_fn} ({kernel})", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": tflops / PEAK_FP32_MFMA_TFLOPS,
                      "traffic": read_traffic()},
         "cpu_baseline": cpu,
         "mlp_train": mlp,
         "parity_sampled_rows_fp64": parity,
+        "vendor_blas": {"what": "torch.mm fp32 (rocBLAS/hipBLASLt), same operands and stream",
+                        "ms": vendor_ms, "tflops": flops / (vendor_ms / 1e3) / 1e12},
     }
     print(json.dumps(line), flush=True)
 

@@ -2,7 +2,7 @@
 
 The product is the native library ``libfastdl_gemm.so`` (HIP kernels behind
 the C-ABI in ``include/fastdl_gemm.h``) and the C++ ``dl::`` API built on it
-(``libdl.so``).  This Python package only loads the C-ABI with ctypes so that
+(``libfastdl.so``).  This Python package only loads the C-ABI with ctypes so that
 tests and ``bench.py`` can drive it with device buffers owned by PyTorch.
 There is no Python or CPU fallback: if the library is missing, importing
 :mod:`fast_dl_amd.capi` raises.
@@ -15,7 +15,9 @@ from .capi import (  # noqa: F401
     EPILOGUE_RELU,
     EPILOGUE_RELU_GRAD,
     KERNEL_AUTO,
+    KERNEL_DMA256,
     KERNEL_SKINNY,
+    KERNEL_SPLITK16,
     KERNEL_SPLITK32,
     KERNEL_TILED64,
     KERNEL_TILED128,

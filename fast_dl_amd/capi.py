@@ -14,10 +14,11 @@ OP_N, OP_T = 0, 1
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_BIAS_RELU, EPILOGUE_RELU, EPILOGUE_RELU_GRAD = range(5)
 KERNEL_AUTO, KERNEL_TILED128, KERNEL_TILED64, KERNEL_SPLITK32, KERNEL_SKINNY = -1, 0, 1, 2, 3
 KERNEL_TILED256, KERNEL_TILED256X128, KERNEL_TILED128W8, KERNEL_SPLITK16 = 4, 5, 6, 7
+KERNEL_DMA256 = 8
 KERNEL_NAMES = {KERNEL_TILED128: "tiled128", KERNEL_TILED64: "tiled64",
                 KERNEL_SPLITK32: "splitk32", KERNEL_SKINNY: "skinny", KERNEL_TILED256: "tiled256",
                 KERNEL_TILED256X128: "tiled256x128", KERNEL_TILED128W8: "tiled128w8",
-                KERNEL_SPLITK16: "splitk16"}
+                KERNEL_SPLITK16: "splitk16", KERNEL_DMA256: "dma256"}
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _LIB = None
@@ -113,6 +114,9 @@ mlp2_graph_launch = _checked("fdl_mlp2_graph_launch")
 mlp2_graph_destroy = _checked("fdl_mlp2_graph_destroy")
 
 
+fill_normal = _checked("fdl_fill_normal")
+
+
 def mlp2_graph_create(*args) -> int:
     """Capture fdl_mlp2_train_step(*args) into a graph; returns the handle (an int)."""
     handle = ctypes.c_void_p()
@@ -121,7 +125,6 @@ def mlp2_graph_create(*args) -> int:
     if status != 0:
         raise FdlError("fdl_mlp2_graph_create", status, lib.fdl_last_error().decode())
     return handle.value
-fill_normal = _checked("fdl_fill_normal")
 
 
 def kernel_choice(transA: int, transB: int, M: int, N: int, K: int, batch: int = 1) -> int:

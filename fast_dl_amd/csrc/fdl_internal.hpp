@@ -48,8 +48,13 @@ enum class GemmKernel : int {
     Tiled256x128 = 5, // 256x128x16 tile, 8 waves of 64x64
     Tiled128W8 = 6,   // 128x128x16 tile, 8 waves of 32x64
     SplitK16 = 7,     // 16x16 output tile (16x16x4 MFMA), K split over waves
+    Dma256 = 8,       // 256x256x16 tile, global -> LDS copies without VGPR staging
     Auto = -1,
 };
+
+// Whether the direct-to-LDS kernel can run this problem (K a multiple of 16,
+// both operands 16-byte vectorisable).
+bool dma_supported(const GemmParams& p, bool transA, bool transB, int64_t batch);
 
 // Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
 hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,

@@ -74,12 +74,19 @@ def test_other_entry_points_validate():
                          1, None, None, 0, 3, None) == -2  # skinny with B transposed
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
                          1, None, None, 0, 9, None) == -1
+    assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 24, 1 << 20, 24, 0, 1 << 20, 16, 0,
+                         1 << 20, 16, 0, 1, None, None, 0, capi.KERNEL_DMA256, None) == -2
     assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
                          *([None] * 11)) == -1
 
 
 def test_kernel_choice():
-    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED256
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_DMA256
+    assert capi.kernel_choice(1, 1, 4096, 4096, 4096) == capi.KERNEL_DMA256
+    # K not a multiple of 16, or B's contiguous extent not a multiple of 4:
+    # the register-staged kernel with the same tile
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4100) == capi.KERNEL_TILED256
+    assert capi.kernel_choice(0, 0, 4096, 4094, 4096) == capi.KERNEL_TILED256
     assert capi.kernel_choice(0, 0, 8, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 8, 4096, 4096) != capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 0, 256, 128, 784) == capi.KERNEL_SPLITK16

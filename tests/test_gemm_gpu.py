@@ -264,6 +264,6 @@ def test_degenerate_sizes(device):
 
 
 def test_kernel_choice_heuristic(device):
-    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_TILED256
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_DMA256
     assert capi.kernel_choice(0, 0, 1, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 1, 4096, 4096) != capi.KERNEL_SKINNY
