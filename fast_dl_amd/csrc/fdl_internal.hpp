@@ -49,12 +49,14 @@ enum class GemmKernel : int {
     Tiled128W8 = 6,   // 128x128x16 tile, 8 waves of 32x64
     SplitK16 = 7,     // 16x16 output tile (16x16x4 MFMA), K split over waves
     Dma256 = 8,       // 256x256x16 tile, global -> LDS copies without VGPR staging
+    Dma128 = 9,       // 128x128x32 tile, global -> LDS copies, two blocks per CU
     Auto = -1,
 };
 
-// Whether the direct-to-LDS kernel can run this problem (K a multiple of 16,
-// both operands 16-byte vectorisable).
-bool dma_supported(const GemmParams& p, bool transA, bool transB, int64_t batch);
+// Whether a direct-to-LDS kernel (Dma256 or Dma128) can run this problem: K a
+// multiple of its K-tile, both operands 16-byte vectorisable.
+bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
+                   int64_t batch);
 
 // Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
 hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,

@@ -393,10 +393,12 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // are clamped to the last valid one: they only feed accumulators that are
 // never stored.
 // ---------------------------------------------------------------------------
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
+          int ILV_ = 0>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int STAGES = STAGES_;
+    static constexpr int XPIPE = XPIPE_, ILV = ILV_;
     static constexpr int NT = kWave * (BM / WM) * (BN / WN);
 };
 
@@ -551,13 +553,41 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         }
     };
 
-    int stage = 0;
-    for (int t = 0; t < ktiles; ++t) {
-        // Loads of tiles t+1 .. t+S-2 may stay in flight; tile t's must land.
-        const int later = min(S - 2, ktiles - 1 - t);
-        if (S >= 4 && later >= 2) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_TILE));
-        } else if (S >= 3 && later >= 1) {
+    auto mfma_group = [&](int slot) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        a[slot][q][mi], b[slot][q][ni], acc[mi][ni], 0, 0, 0);
+    };
+    // With ILV the scheduler is asked to spread the LDS reads of the next
+    // group between this group's MFMAs (two MFMAs, one read, ...).
+    auto interleave_hint = [&]() {
+        if (Cfg::ILV) {
+            constexpr int kReads = FM + 2 * FN;  // b128 A reads + paired b32 B reads
+            constexpr int kMfma = 4 * FM * FN;
+#pragma unroll
+            for (int j = 0; j < kReads; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, kMfma - 2 * kReads, 0);
+        }
+    };
+
+    if (Cfg::XPIPE) {
+        // Cross-tile pipeline (two stages): the barrier sits before the last
+        // group's MFMAs, so the first reads of tile t+1 are in flight while
+        // those MFMAs run.  At the barrier every wave has read all of tile t
+        // (lgkmcnt 0) and tile t+1 has landed (vmcnt 0: it is the only copy in
+        // flight), so tile t+2 can go into tile t's stage right after it.
+        static_assert(S == 2 && NG % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
+        if (ktiles > 1) {
+            opa.issue(A, p.lda, BK, As + OpA::STAGE);
+            opb.issue(B, p.ldb, BK, Bs + OpB::STAGE);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_TILE));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -565,29 +595,69 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (t + S - 1 < ktiles) {
-            const int ns = stage == 0 ? S - 1 : stage - 1;  // (t + S - 1) % S
-            opa.issue(A, p.lda, (t + S - 1) * BK, As + ns * OpA::STAGE);
-            opb.issue(B, p.ldb, (t + S - 1) * BK, Bs + ns * OpB::STAGE);
-        }
-        const float* as = As + stage * OpA::STAGE;
-        const float* bs = Bs + stage * OpB::STAGE;
-        read_group(as, bs, 0, 0);
+        read_group(As, Bs, 0, 0);
+        for (int t = 0; t < ktiles; ++t) {
+            const int cur = t & 1;
+            const float* as = As + cur * OpA::STAGE;
+            const float* bs = Bs + cur * OpB::STAGE;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            if (g + 1 < NG) read_group(as, bs, g + 1, (g + 1) & 1);
+            for (int g = 0; g + 1 < NG; ++g) {
+                __builtin_amdgcn_sched_barrier(0);
+                read_group(as, bs, g + 1, (g + 1) & 1);
+                mfma_group(g & 1);
+                interleave_hint();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // vmcnt(0) lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (t + 2 < ktiles) {
+                opa.issue(A, p.lda, (t + 2) * BK, As + cur * OpA::STAGE);
+                opb.issue(B, p.ldb, (t + 2) * BK, Bs + cur * OpB::STAGE);
+            }
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-                    for (int ni = 0; ni < FN; ++ni)
-                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            a[g & 1][q][mi], b[g & 1][q][ni], acc[mi][ni], 0, 0, 0);
+            if (t + 1 < ktiles) {
+                read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0);
+            }
+            mfma_group((NG - 1) & 1);
+            interleave_hint();
             __builtin_amdgcn_sched_barrier(0);
         }
-        stage = stage + 1 == S ? 0 : stage + 1;
+    } else {
+        int stage = 0;
+        for (int t = 0; t < ktiles; ++t) {
+            // Loads of tiles t+1 .. t+S-2 may stay in flight; tile t's must land.
+            const int later = min(S - 2, ktiles - 1 - t);
+            if (S >= 4 && later >= 2) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_TILE));
+            } else if (S >= 3 && later >= 1) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_TILE));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (t + S - 1 < ktiles) {
+                const int ns = stage == 0 ? S - 1 : stage - 1;  // (t + S - 1) % S
+                opa.issue(A, p.lda, (t + S - 1) * BK, As + ns * OpA::STAGE);
+                opb.issue(B, p.ldb, (t + S - 1) * BK, Bs + ns * OpB::STAGE);
+            }
+            const float* as = As + stage * OpA::STAGE;
+            const float* bs = Bs + stage * OpB::STAGE;
+            read_group(as, bs, 0, 0);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (g + 1 < NG) read_group(as, bs, g + 1, (g + 1) & 1);
+                if (!Cfg::ILV) __builtin_amdgcn_sched_barrier(0);
+                mfma_group(g & 1);
+                if (g + 1 < NG) interleave_hint();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            stage = stage + 1 == S ? 0 : stage + 1;
+        }
     }
 
     store_wave_tile<FM, FN>(acc, p, bz, m0 + wm0, n0 + wn0, half, l32);
@@ -1166,7 +1236,13 @@ using CfgTiled64 = TileCfg<64, 64, 16, 32, 32, 4, 1>;
 using CfgTiled256 = TileCfg<256, 256, 16, 128, 64, 4, 1, 0, 2, 1, 1>;
 using CfgTiled256x128 = TileCfg<256, 128, 16, 64, 64, 4, 1>;
 using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
-using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2>;
+// Direct-to-LDS configurations: two stages with the cross-tile pipeline and
+// interleaved fragment reads (4096^3: 1.00-1.05 ms; 8192^3: 7.78 ms, 141
+// TFLOP/s).  The 128x128 tile runs two blocks per CU and wins where 256x256
+// tiles would leave CUs idle (2048^3: 0.161 vs 0.178 ms for Tiled128W8;
+// 4000x3000x2048: 0.45 vs 0.54 ms for the 256x256 tile).
+using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
+using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
 
 // Dispatch cost model.  A config runs `slots` blocks per CU at full
 // occupancy (LDS and register bound), each block holding `waves` waves; eff[w]
@@ -1181,9 +1257,11 @@ struct TileModel {
 };
 
 constexpr TileModel kTileModels[] = {
+    {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f}},
+    {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.67f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f}},
     {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
-    {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.72f, 0.80f, 0.80f, 0.80f, 0.80f, 0.80f, 0.80f}},
+    {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.66f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f}},
     {GemmKernel::Tiled128W8, 128, 128, 3, 8, {0, 0.45f, 0.63f, 0.68f, 0.72f, 0.74f, 0.75f, 0.75f, 0.75f}},
     {GemmKernel::Tiled64, 64, 64, 8, 4, {0, 0.30f, 0.45f, 0.52f, 0.60f, 0.63f, 0.65f, 0.67f, 0.68f}},
 };
@@ -1204,18 +1282,22 @@ double predicted_time(const TileModel& t, int M, int N, int64_t batch) {
     return time;
 }
 
-// Shape part of the direct-to-LDS kernel's contract (pointers not needed).
-bool dma_shape_ok(const GemmParams& p, bool transA, bool transB) {
+bool is_dma(GemmKernel k) { return k == GemmKernel::Dma256 || k == GemmKernel::Dma128; }
+
+// Shape part of a direct-to-LDS kernel's contract (pointers not needed).
+bool dma_shape_ok(GemmKernel k, const GemmParams& p, bool transA, bool transB) {
+    const int bk = k == GemmKernel::Dma256 ? CfgDma256::BK : CfgDma128::BK;
     const int64_t a_contig = transA ? p.M : p.K;
     const int64_t b_contig = transB ? p.K : p.N;
-    return p.K >= 16 && p.K % 16 == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
+    return p.K >= bk && p.K % bk == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
            p.lda % 4 == 0 && p.ldb % 4 == 0;
 }
 
 }  // namespace
 
-bool dma_supported(const GemmParams& p, bool transA, bool transB, int64_t batch) {
-    return dma_shape_ok(p, transA, transB) &&
+bool dma_supported(GemmKernel k, const GemmParams& p, bool transA, bool transB,
+                   int64_t batch) {
+    return is_dma(k) && dma_shape_ok(k, p, transA, transB) &&
            vec_ok(p.A, transA ? p.M : p.K, p.lda, p.strideA, batch) &&
            vec_ok(p.B, transB ? p.K : p.N, p.ldb, p.strideB, batch);
 }
@@ -1231,6 +1313,7 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::Tiled128W8: return "tiled128w8";
         case GemmKernel::SplitK16: return "splitk16";
         case GemmKernel::Dma256: return "dma256";
+        case GemmKernel::Dma128: return "dma128";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -1258,18 +1341,16 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     double best_time = 0.0;
     bool first = true;
     for (const TileModel& t : kTileModels) {
+        // The direct-to-LDS kernels compete only where their shape contract
+        // holds; launch_sgemm falls back to the register-staged kernel with
+        // the same tile when the pointers are not 16-byte aligned.
+        if (is_dma(t.kernel) && !dma_shape_ok(t.kernel, p, transA, transB)) continue;
         const double tm = predicted_time(t, p.M, p.N, batch);
         if (first || tm < best_time * 0.99) {  // ties keep the earlier (larger) tile
             best = t.kernel;
             best_time = tm;
             first = false;
         }
-    }
-    // Same 256x256 tile without VGPR staging: 2-4% faster where it applies
-    // (4096^3: 1.07-1.09 vs 1.10-1.12 ms).  launch_sgemm falls back to the
-    // register-staged kernel when the pointers are not 16-byte aligned.
-    if (best == GemmKernel::Tiled256 && dma_shape_ok(p, transA, transB)) {
-        best = GemmKernel::Dma256;
     }
     return best;
 }
@@ -1280,9 +1361,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
     const bool automatic = kernel == GemmKernel::Auto;
     if (automatic) kernel = choose_kernel(p0, transA, transB, batch);
     if (kernel == GemmKernel::Skinny && (transB || p0.M > 8)) return hipErrorInvalidValue;
-    if (kernel == GemmKernel::Dma256 && !dma_supported(p0, transA, transB, batch)) {
+    if (is_dma(kernel) && !dma_supported(kernel, p0, transA, transB, batch)) {
         if (!automatic) return hipErrorInvalidValue;
-        kernel = GemmKernel::Tiled256;
+        kernel = kernel == GemmKernel::Dma256 ? GemmKernel::Tiled256 : GemmKernel::Tiled128;
     }
 
     const bool va = vec_ok(p0.A, transA ? p0.M : p0.K, p0.lda, p0.strideA, batch);
@@ -1323,6 +1404,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::Dma256:
                 err = launch_dma<CfgDma256>(p, transA, transB, nb, stream);
+                break;
+            case GemmKernel::Dma128:
+                err = launch_dma<CfgDma128>(p, transA, transB, nb, stream);
                 break;
             default:
                 return hipErrorInvalidValue;

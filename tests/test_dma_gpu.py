@@ -1,8 +1,9 @@
-"""GPU parity of the direct-to-LDS kernel (FDL_KERNEL_DMA256) and of its
-dispatch rules: it runs only where K is a multiple of 16 and both operands are
-16-byte vectorisable, refuses other problems with FDL_ERROR_NOT_SUPPORTED when
-forced, and the automatic choice falls back to the register-staged 256x256
-kernel for misaligned pointers."""
+"""GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256, K-tile 16, and
+FDL_KERNEL_DMA128, K-tile 32) and of their dispatch rules: they run only where
+K is a multiple of the K-tile and both operands are 16-byte vectorisable,
+refuse other problems with FDL_ERROR_NOT_SUPPORTED when forced, and the
+automatic choice falls back to the register-staged kernel with the same tile
+for misaligned pointers."""
 import numpy as np
 import pytest
 
@@ -12,61 +13,67 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, s
 pytestmark = pytest.mark.gpu
 
 DMA = capi.KERNEL_DMA256
+DMAS = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32)]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 # M and N multiples of 4 (either may be the contiguous extent), ragged against
-# the 256x256 tile; K multiples of 16 covering 1, 2, 3 and many K-tiles.
-SHAPES = [(4, 4, 16), (256, 256, 32), (260, 300, 48), (516, 260, 272), (64, 1000, 96),
-          (768, 512, 1024)]
+# the tiles; K in K-tiles (16 or 32 each) covering 1, 2, 3 and many K-tiles.
+SHAPES = [(4, 4, 1), (256, 256, 2), (260, 300, 3), (516, 260, 17), (64, 1000, 6),
+          (768, 512, 64)]
 
 
 def _rng(*key):
     return np.random.default_rng(abs(hash(key)) & 0xFFFFFFFF)
 
 
+@pytest.mark.parametrize("fam,bk", DMAS)
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
-@pytest.mark.parametrize("M,N,K", SHAPES)
-def test_dma_layouts_and_edges(device, ta, tb, M, N, K):
+@pytest.mark.parametrize("M,N,kt", SHAPES)
+def test_dma_layouts_and_edges(device, fam, bk, ta, tb, M, N, kt):
+    K = kt * bk
     A, B = operands(_rng(M, N, K, ta, tb), ta, tb, M, N, K, 1)
-    say(f"dma256 ta={ta} tb={tb} M={M} N={N} K={K}")
-    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=DMA)
+    say(f"dma fam={fam} ta={ta} tb={tb} M={M} N={N} K={K}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=fam)
     check_gemm(c, ta, tb, A, B, M, N, K)
 
 
+@pytest.mark.parametrize("fam,bk", DMAS)
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
-def test_dma_integer_inputs_bit_exact(device, ta, tb):
-    M, N, K = 300, 260, 400
+def test_dma_integer_inputs_bit_exact(device, fam, bk, ta, tb):
+    M, N, K = 300, 260, 416
     A, B = operands(_rng(7, ta, tb), ta, tb, M, N, K, 1, dist="int")
-    say(f"dma256 integer exact ta={ta} tb={tb}")
-    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=DMA)[0]
+    say(f"dma integer exact fam={fam} ta={ta} tb={tb}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=fam)[0]
     opA = (A[0].T if ta else A[0]).astype(np.int64)
     opB = (B[0].T if tb else B[0]).astype(np.int64)
     assert np.array_equal(c, (opA @ opB).astype(np.float32))
 
 
+@pytest.mark.parametrize("fam,bk", DMAS)
 @pytest.mark.parametrize("epi", [capi.EPILOGUE_BIAS, capi.EPILOGUE_BIAS_RELU,
                                  capi.EPILOGUE_RELU, capi.EPILOGUE_RELU_GRAD])
-def test_dma_epilogues(device, epi):
+def test_dma_epilogues(device, fam, bk, epi):
     M, N, K = 520, 264, 160
     g = _rng(11, epi)
     A, B = operands(g, 0, 0, M, N, K, 1)
     bias = (g.standard_normal(N) * 0.5).astype(np.float32)
     aux = g.standard_normal((M, N)).astype(np.float32)
-    say(f"dma256 epilogue {epi}")
-    c = gpu_sgemm(0, 0, A, B, M, N, K, bias=bias, aux=aux, epilogue=epi, kernel=DMA)
+    say(f"dma epilogue fam={fam} epi={epi}")
+    c = gpu_sgemm(0, 0, A, B, M, N, K, bias=bias, aux=aux, epilogue=epi, kernel=fam)
     check_gemm(c, 0, 0, A, B, M, N, K, bias=bias, aux=aux, epilogue=epi)
 
 
-def test_dma_batched_and_padded_ld(device):
+@pytest.mark.parametrize("fam,bk", DMAS)
+def test_dma_batched_and_padded_ld(device, fam, bk):
     M, N, K, batch = 260, 264, 64, 3
     A, B = operands(_rng(13), 0, 1, M, N, K, batch)
-    say("dma256 batched NT, padded lda/ldb/ldc")
+    say(f"dma batched NT, padded lda/ldb/ldc fam={fam}")
     # lda/ldb padded to the next multiple of 4 beyond K, ldc beyond N
     lda, ldb, ldc = K + 8, K + 4, N + 12
     Ap = np.zeros((batch, M, lda), np.float32)
     Ap[:, :, :K] = A
     Bp = np.zeros((batch, N, ldb), np.float32)
     Bp[:, :, :K] = B
-    c = gpu_sgemm(0, 1, Ap, Bp, M, N, K, batch=batch, kernel=DMA, lda=lda, ldb=ldb, ldc=ldc)
+    c = gpu_sgemm(0, 1, Ap, Bp, M, N, K, batch=batch, kernel=fam, lda=lda, ldb=ldb, ldc=ldc)
     check_gemm(c, 0, 1, A, B, M, N, K, batch=batch)
 
 
@@ -84,8 +91,12 @@ def test_dma_refuses_unsupported_problems(device):
     # K not a multiple of 16
     assert _raw_select(0, 0, 64, 64, 24, p, 24, p, 64, p, DMA) == -2
     assert "dma256" in capi.last_error()
+    # K a multiple of 16 but not of the 128x128 kernel's K-tile of 32
+    assert _raw_select(0, 0, 64, 64, 48, p, 48, p, 64, p, capi.KERNEL_DMA128) == -2
+    assert "dma128" in capi.last_error()
     # A misaligned by one float
     assert _raw_select(0, 0, 64, 64, 32, p + 4, 32, p, 64, p, DMA) == -2
+    assert _raw_select(0, 0, 64, 64, 32, p + 4, 32, p, 64, p, capi.KERNEL_DMA128) == -2
     # ld not a multiple of 4
     assert _raw_select(0, 0, 64, 64, 32, p, 33, p, 64, p, DMA) == -2
     # N (B's contiguous extent) not a multiple of 4
