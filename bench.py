@@ -28,6 +28,23 @@ PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix peak (256 CU x 256 FLO
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sgemm_nn_4096_traffic.txt")
 
+# --profile-mode workloads: name -> (M, N, K, transB, batch, epilogue, rotate).
+# "headline" is the bench line's own GEMM (M = N = K = --size).
+PROFILE_CONFIGS = {
+    "headline": None,
+    "c1": (256, 128, 784, 0, 1, 0, 1),
+    "c3_1024": (1024, 1024, 1024, 0, 1, 0, 1),
+    "c3_2048": (2048, 2048, 2048, 0, 1, 0, 1),
+    "c3_8192": (8192, 8192, 8192, 0, 1, 0, 1),
+    "c4_nn": (128, 128, 64, 0, 64, 0, 40),
+    "c4_nt": (128, 128, 64, 1, 64, 0, 40),
+    "c5a_m1": (1, 4096, 4096, 0, 1, 2, 6),
+    "c5a_m8": (8, 4096, 4096, 0, 1, 2, 6),
+    "c5b_777": (777, 777, 777, 0, 1, 2, 1),
+    "c5b_1000": (1000, 1000, 1000, 0, 1, 2, 1),
+    "c2_mlp": "mlp",
+}
+
 
 def parse_args():
     ap = argparse.ArgumentParser()
@@ -40,6 +57,8 @@ def parse_args():
     ap.add_argument("--sweep", default=None, help="write every BASELINE config's timing here")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the headline launches (for rocprofv3 runs)")
+    ap.add_argument("--profile-config", default="headline", choices=sorted(PROFILE_CONFIGS),
+                    help="with --profile-mode: which BASELINE configuration to launch")
     ap.add_argument("--copy-calib", action="store_true",
                     help="with --profile-mode: also run a 256 MiB device copy, the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -337,9 +356,21 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    if args.profile_mode and args.profile_config != "headline":
+        cfg = PROFILE_CONFIGS[args.profile_config]
+        if cfg == "mlp":
+            _, pms, _, _, _ = mlp_rate(capi, torch, steps=args.steps, warmup=args.warmup)
+        else:
+            M, N, K, tb, batch, epi, rot = cfg
+            plaunch, *_ = gemm_case(capi, torch, M, N, K, tb=tb, batch=batch, epi=epi,
+                                    rotate=rot)
+            pms = time_launches(plaunch, args.steps, args.warmup, stream)
+        print(json.dumps({"profile_mode": True, "config": args.profile_config,
+                          "ms_per_launch": pms}), flush=True)
+        return
     n = args.size
     launch, A, B, C = gemm_case(capi, torch, n, n, n, seed=0)
-    stream = torch.cuda.current_stream()
     ms = time_launches(launch, args.steps, args.warmup, stream)
     if args.profile_mode:
         if args.copy_calib:
@@ -353,7 +384,7 @@ def main():
     flops = 2.0 * n * n * n
     tflops = flops / (ms / 1e3) / 1e12
     med, p10, p90 = launch_percentiles(launch, args.steps, stream)
-    vendor_ms = time_launches(vendor_case(torch, n, n, n), max(10, args.steps // 5), 3, stream)
+    vendor_ms = time_launches(vendor_case(torch, n, n, n), args.steps, args.warmup, stream)
     parity = sampled_parity(A, B, C, n)
 
     mlp = None
