@@ -50,11 +50,12 @@ enum class GemmKernel : int {
     SplitK16 = 7,     // 16x16 output tile (16x16x4 MFMA), K split over waves
     Dma256 = 8,       // 256x256x16 tile, global -> LDS copies without VGPR staging
     Dma128 = 9,       // 128x128x32 tile, global -> LDS copies, two blocks per CU
+    Dma64 = 10,       // 64x64x64 tile, global -> LDS copies, four waves of 32x32
     Auto = -1,
 };
 
-// Whether a direct-to-LDS kernel (Dma256 or Dma128) can run this problem: K a
-// multiple of its K-tile, both operands 16-byte vectorisable.
+// Whether a direct-to-LDS kernel (Dma256, Dma128, Dma64) can run this problem:
+// K a multiple of 4, both operands 16-byte vectorisable.
 bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
                    int64_t batch);
 

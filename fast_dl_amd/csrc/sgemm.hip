@@ -387,11 +387,11 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // same permutation for both operands, so every k is summed exactly once and
 // a lane's four A (or B) values of a group are one contiguous chunk.
 //
-// Host contract: K is a multiple of BK; the operands satisfy the 16-byte
-// vector conditions (base, ld and batch stride multiples of 4 floats; an
-// mn-contiguous operand's extent a multiple of 4).  Rows (columns) past M (N)
-// are clamped to the last valid one: they only feed accumulators that are
-// never stored.
+// Host contract: K is a multiple of 4 (the last K-tile may be partial) and
+// the operands satisfy the 16-byte vector conditions (base, ld and batch
+// stride multiples of 4 floats; an mn-contiguous operand's extent a multiple
+// of 4).  Rows (columns) past M (N) are clamped to the last valid one: they
+// only feed accumulators that are never stored.
 // ---------------------------------------------------------------------------
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
           int ILV_ = 0>
@@ -420,8 +420,10 @@ __device__ __forceinline__ void dma_copy16(const float* g, float* lds) {
 // extra LDS cycles, and with ((r >> 1) ^ (r >> 3)) & 3 it costs 17%).
 template <int CPR>
 __device__ __forceinline__ int kc_swz(int r) {
-    static_assert(CPR == 4 || CPR == 8, "4 or 8 chunks per row");
-    return CPR == 4 ? (r >> 2) & 3 : (r ^ (r >> 3)) & 7;
+    static_assert(CPR == 4 || CPR == 8 || CPR == 16, "4, 8 or 16 chunks per row");
+    if (CPR == 4) return (r >> 2) & 3;
+    if (CPR == 8) return (r ^ (r >> 3)) & 7;
+    return r & 15;  // 16 chunks: measured conflict-free, (r >> 1) & 15 costs 10%
 }
 
 template <int MN, int BK, int NT, bool KC>
@@ -433,7 +435,8 @@ struct DmaOperand {
     static constexpr int PER = CHUNKS / NT;                // copies per lane per tile
     static constexpr int ROW_CHUNKS = MN / 4;              // chunks per mn-contiguous row
     static_assert(CHUNKS % NT == 0, "copies must divide evenly");
-    static_assert(!KC || CPR == 4 || CPR == 8, "BK of 16 or 32 for a k-contiguous operand");
+    static_assert(!KC || CPR == 4 || CPR == 8 || CPR == 16,
+                  "BK of 16, 32 or 64 for a k-contiguous operand");
     static_assert(KC || (kWave % ROW_CHUNKS == 0 || ROW_CHUNKS % kWave == 0),
                   "mn-contiguous rows must tile the 64-lane copies");
     int64_t goff[PER];  // this lane's global offset of each copy at k0 = 0
@@ -459,12 +462,34 @@ struct DmaOperand {
         }
     }
 
-    // Copies the tile whose first reduction index is k0 into `stage`.
+    // Copies the tile whose first reduction index is k0 into `stage`.  In
+    // the tile that crosses K (K a multiple of 4, so a chunk is either wholly
+    // inside or wholly past K) the copies past K are redirected to the last
+    // valid chunk or row: the kernel zeroes the fragment values read from
+    // those slots, so they never count.
     __device__ __forceinline__ void issue(const float* __restrict__ base, int64_t ld, int k0,
-                                          float* stage) const {
-        const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
+                                          int K, float* stage, int tid) const {
+        if (k0 + BK <= K) {
+            const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) dma_copy16(base + goff[i] + koff, stage + loff[i]);
+            for (int i = 0; i < PER; ++i) dma_copy16(base + goff[i] + koff, stage + loff[i]);
+            return;
+        }
+        const int lane = tid & (kWave - 1);
+        const int wave = tid / kWave;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int slot = (wave * PER + i) * kWave + lane;
+            int64_t off;
+            if (KC) {
+                const int kc = 4 * ((slot % CPR) ^ kc_swz<CPR>(slot / CPR));
+                off = goff[i] - kc + min(k0 + kc, K - 4);
+            } else {
+                const int kr = slot / ROW_CHUNKS;
+                off = goff[i] + (int64_t)(min(k0 + kr, K - 1) - kr) * ld;
+            }
+            dma_copy16(base + off, stage + loff[i]);
+        }
     }
 
     // Operand values of MFMA q of group g for fragment row/col `idx` (the
@@ -526,18 +551,25 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
 
-    const int ktiles = p.K / BK;
+    // K need only be a multiple of 4: the last K-tile may be partial.
+    const int ktiles = (p.K + BK - 1) / BK;
+    const int tail_tile = (p.K % BK) ? ktiles - 1 : -1;
+    auto issue_tile = [&](int t, int s) {
+        opa.issue(A, p.lda, t * BK, p.K, As + s * OpA::STAGE, tid);
+        opb.issue(B, p.ldb, t * BK, p.K, Bs + s * OpB::STAGE, tid);
+    };
 #pragma unroll
     for (int s = 0; s < S - 1; ++s) {
-        if (s < ktiles) {
-            opa.issue(A, p.lda, s * BK, As + s * OpA::STAGE);
-            opb.issue(B, p.ldb, s * BK, Bs + s * OpB::STAGE);
-        }
+        if (s < ktiles) issue_tile(s, s);
     }
 
     float a[2][4][FM];
     float b[2][4][FN];
-    auto read_group = [&](const float* as, const float* bs, int g, int slot) {
+    // Reads group g of tile `tile` into register slot `slot`; in the tile
+    // that crosses K, A and B values at k >= K are zeroed (the LDS slots past
+    // K hold redirected copies of valid data; zeroing both keeps an infinity
+    // there from turning into 0 * inf).
+    auto read_group = [&](const float* as, const float* bs, int g, int slot, int tile) {
         float v[4];
 #pragma unroll
         for (int mi = 0; mi < FM; ++mi) {
@@ -550,6 +582,18 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             opb.read(bs, g, wn0 + ni * 32 + l32, half, v);
 #pragma unroll
             for (int q = 0; q < 4; ++q) b[slot][q][ni] = v[q];
+        }
+        if (tile == tail_tile) {
+            const int kbase = tile * BK + 8 * g + 4 * half;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int mi = 0; mi < FM; ++mi)
+                    a[slot][q][mi] = kbase + q < p.K ? a[slot][q][mi] : 0.0f;
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+                    b[slot][q][ni] = kbase + q < p.K ? b[slot][q][ni] : 0.0f;
+            }
         }
     };
 
@@ -569,16 +613,19 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         if (Cfg::ILV) {
             constexpr int kReads = FM + 2 * FN;  // b128 A reads + paired b32 B reads
             constexpr int kMfma = 4 * FM * FN;
+            constexpr int kPer = kMfma >= 2 * kReads ? 2 : 1;
+            constexpr int kPairs = kMfma / kPer < kReads ? kMfma / kPer : kReads;
 #pragma unroll
-            for (int j = 0; j < kReads; ++j) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            for (int j = 0; j < kPairs; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, kMfma - 2 * kReads, 0);
+            if (kMfma > kPer * kPairs)
+                __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPer * kPairs, 0);
         }
     };
 
-    if (Cfg::XPIPE) {
+    if constexpr (Cfg::XPIPE != 0) {
         // Cross-tile pipeline (two stages): the barrier sits before the last
         // group's MFMAs, so the first reads of tile t+1 are in flight while
         // those MFMAs run.  At the barrier every wave has read all of tile t
@@ -586,8 +633,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         // flight), so tile t+2 can go into tile t's stage right after it.
         static_assert(S == 2 && NG % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
         if (ktiles > 1) {
-            opa.issue(A, p.lda, BK, As + OpA::STAGE);
-            opb.issue(B, p.ldb, BK, Bs + OpB::STAGE);
+            issue_tile(1, 1);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_TILE));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -595,7 +641,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        read_group(As, Bs, 0, 0);
+        read_group(As, Bs, 0, 0, 0);
         for (int t = 0; t < ktiles; ++t) {
             const int cur = t & 1;
             const float* as = As + cur * OpA::STAGE;
@@ -603,7 +649,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
 #pragma unroll
             for (int g = 0; g + 1 < NG; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                read_group(as, bs, g + 1, (g + 1) & 1);
+                read_group(as, bs, g + 1, (g + 1) & 1, t);
                 mfma_group(g & 1);
                 interleave_hint();
                 __builtin_amdgcn_sched_barrier(0);
@@ -612,13 +658,10 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (t + 2 < ktiles) {
-                opa.issue(A, p.lda, (t + 2) * BK, As + cur * OpA::STAGE);
-                opb.issue(B, p.ldb, (t + 2) * BK, Bs + cur * OpB::STAGE);
-            }
+            if (t + 2 < ktiles) issue_tile(t + 2, cur);
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < ktiles) {
-                read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0);
+                read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1);
             }
             mfma_group((NG - 1) & 1);
             interleave_hint();
@@ -640,17 +683,15 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             if (t + S - 1 < ktiles) {
-                const int ns = stage == 0 ? S - 1 : stage - 1;  // (t + S - 1) % S
-                opa.issue(A, p.lda, (t + S - 1) * BK, As + ns * OpA::STAGE);
-                opb.issue(B, p.ldb, (t + S - 1) * BK, Bs + ns * OpB::STAGE);
+                issue_tile(t + S - 1, stage == 0 ? S - 1 : stage - 1);  // (t + S - 1) % S
             }
             const float* as = As + stage * OpA::STAGE;
             const float* bs = Bs + stage * OpB::STAGE;
-            read_group(as, bs, 0, 0);
+            read_group(as, bs, 0, 0, t);
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                if (g + 1 < NG) read_group(as, bs, g + 1, (g + 1) & 1);
+                if (g + 1 < NG) read_group(as, bs, g + 1, (g + 1) & 1, t);
                 if (!Cfg::ILV) __builtin_amdgcn_sched_barrier(0);
                 mfma_group(g & 1);
                 if (g + 1 < NG) interleave_hint();
@@ -1243,6 +1284,9 @@ using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
 // 4000x3000x2048: 0.45 vs 0.54 ms for the 256x256 tile).
 using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
 using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
+// 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU
+// (1024^3: 29.7 us vs 42 us for the split-K kernel; 1000^3: 30 vs 43 us).
+using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1>;
 
 // Dispatch cost model.  A config runs `slots` blocks per CU at full
 // occupancy (LDS and register bound), each block holding `waves` waves; eff[w]
@@ -1259,6 +1303,7 @@ struct TileModel {
 constexpr TileModel kTileModels[] = {
     {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f}},
     {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.67f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f}},
+    {GemmKernel::Dma64, 64, 64, 2, 4, {0, 0.46f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f}},
     {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.66f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f}},
@@ -1282,14 +1327,16 @@ double predicted_time(const TileModel& t, int M, int N, int64_t batch) {
     return time;
 }
 
-bool is_dma(GemmKernel k) { return k == GemmKernel::Dma256 || k == GemmKernel::Dma128; }
+bool is_dma(GemmKernel k) {
+    return k == GemmKernel::Dma256 || k == GemmKernel::Dma128 || k == GemmKernel::Dma64;
+}
 
 // Shape part of a direct-to-LDS kernel's contract (pointers not needed).
 bool dma_shape_ok(GemmKernel k, const GemmParams& p, bool transA, bool transB) {
-    const int bk = k == GemmKernel::Dma256 ? CfgDma256::BK : CfgDma128::BK;
+    (void)k;
     const int64_t a_contig = transA ? p.M : p.K;
     const int64_t b_contig = transB ? p.K : p.N;
-    return p.K >= bk && p.K % bk == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
+    return p.K >= 4 && p.K % 4 == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
            p.lda % 4 == 0 && p.ldb % 4 == 0;
 }
 
@@ -1314,6 +1361,7 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::SplitK16: return "splitk16";
         case GemmKernel::Dma256: return "dma256";
         case GemmKernel::Dma128: return "dma128";
+        case GemmKernel::Dma64: return "dma64";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -1329,11 +1377,13 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     // Too few 64x64 tiles to occupy the GPU, or too short a K loop to
     // amortise LDS staging: split K over the waves of a block instead, with
     // 16x16 output tiles when 32x32 ones would leave most CUs idle.
-    // Below ~128 tiles of 128x128 the LDS-tiled kernels cannot fill the GPU
-    // and the split-K kernels measure faster (1024^3: 34 vs 42 us; the C4
-    // batch of 64 128x128x64 problems: 5.8 vs 6.8 us).
+    // Below ~128 tiles of 128x128 the register-staged tile kernels cannot fill
+    // the GPU and the split-K kernels measure faster (the C4 batch of 64
+    // 128x128x64 problems: 5.8 vs 6.8 us); the 64x64 direct-to-LDS tile beats
+    // them once K is long enough (1024^3: 29.7 vs 42 us).
     const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (t64 < kCUs || p.K < 64 || t128 < 128) {
+    const bool dma_mid = p.K >= 256 && dma_shape_ok(GemmKernel::Dma64, p, transA, transB);
+    if (t64 < kCUs || p.K < 64 || (t128 < 128 && !dma_mid)) {
         const int64_t t32 = (int64_t)((p.M + 31) / 32) * ((p.N + 31) / 32) * batch;
         return t32 < 128 ? GemmKernel::SplitK16 : GemmKernel::SplitK32;
     }
@@ -1363,7 +1413,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
     if (kernel == GemmKernel::Skinny && (transB || p0.M > 8)) return hipErrorInvalidValue;
     if (is_dma(kernel) && !dma_supported(kernel, p0, transA, transB, batch)) {
         if (!automatic) return hipErrorInvalidValue;
-        kernel = kernel == GemmKernel::Dma256 ? GemmKernel::Tiled256 : GemmKernel::Tiled128;
+        kernel = kernel == GemmKernel::Dma256   ? GemmKernel::Tiled256
+                 : kernel == GemmKernel::Dma128 ? GemmKernel::Tiled128
+                                                : GemmKernel::Tiled64;
     }
 
     const bool va = vec_ok(p0.A, transA ? p0.M : p0.K, p0.lda, p0.strideA, batch);
@@ -1407,6 +1459,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::Dma128:
                 err = launch_dma<CfgDma128>(p, transA, transB, nb, stream);
+                break;
+            case GemmKernel::Dma64:
+                err = launch_dma<CfgDma64>(p, transA, transB, nb, stream);
                 break;
             default:
                 return hipErrorInvalidValue;

@@ -97,11 +97,11 @@ typedef enum fdl_kernel {
     FDL_KERNEL_TILED128W8 = 6, /* 128x128x16 tile, 8 waves of 32x64                 */
     FDL_KERNEL_SPLITK16 = 7,   /* 16x16 tile (16x16x4 MFMA), K split over waves     */
     FDL_KERNEL_DMA256 = 8,     /* 256x256x16 tile fed by direct global->LDS copies;
-                                  needs K % 16 == 0 and 16-byte-vectorisable operands
+                                  needs K % 4 == 0 and 16-byte-vectorisable operands
                                   (base, ld and batch stride multiples of 4 floats,
                                   the contiguous extent a multiple of 4)          */
-    FDL_KERNEL_DMA128 = 9      /* 128x128x32 tile, two blocks per CU, same copies;
-                                  needs K % 32 == 0 and vectorisable operands     */
+    FDL_KERNEL_DMA128 = 9,     /* 128x128x32 tile, two blocks per CU, same copies  */
+    FDL_KERNEL_DMA64 = 10      /* 64x64x64 tile, four waves of 32x32, same copies  */
 } fdl_kernel;
 
 /*

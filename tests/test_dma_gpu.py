@@ -1,9 +1,10 @@
-"""GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256, K-tile 16, and
-FDL_KERNEL_DMA128, K-tile 32) and of their dispatch rules: they run only where
-K is a multiple of the K-tile and both operands are 16-byte vectorisable,
-refuse other problems with FDL_ERROR_NOT_SUPPORTED when forced, and the
-automatic choice falls back to the register-staged kernel with the same tile
-for misaligned pointers."""
+"""GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256, K-tile 16;
+FDL_KERNEL_DMA128, K-tile 32; FDL_KERNEL_DMA64, K-tile 64) and of their
+dispatch rules: they run where K is a multiple of 4 (a partial last K-tile is
+clamped and masked) and both operands are 16-byte vectorisable, refuse other
+problems with FDL_ERROR_NOT_SUPPORTED when forced, and the automatic choice
+falls back to the register-staged kernel with the same tile for misaligned
+pointers."""
 import numpy as np
 import pytest
 
@@ -13,7 +14,7 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, s
 pytestmark = pytest.mark.gpu
 
 DMA = capi.KERNEL_DMA256
-DMAS = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32)]
+DMAS = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32), (capi.KERNEL_DMA64, 64)]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 # M and N multiples of 4 (either may be the contiguous extent), ragged against
 # the tiles; K in K-tiles (16 or 32 each) covering 1, 2, 3 and many K-tiles.
@@ -82,25 +83,51 @@ def _raw_select(ta, tb, M, N, K, a_ptr, lda, b_ptr, ldb, c_ptr, kernel):
                          c_ptr, N, 0, 1, None, None, 0, kernel, stream())
 
 
+@pytest.mark.parametrize("fam,bk", DMAS)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+@pytest.mark.parametrize("K", [4, 20, 100, 1000])
+def test_dma_partial_last_k_tile(device, fam, bk, ta, tb, K):
+    # K a multiple of 4 but not of the K-tile: the last tile's copies past K
+    # are redirected and masked.  Non-finite values right at the end of K in
+    # the other operand must not leak into the masked slots as 0 * inf.
+    M, N = 132, 200
+    A, B = operands(_rng(K, ta, tb, fam), ta, tb, M, N, K, 1)
+    say(f"dma partial K-tile fam={fam} ta={ta} tb={tb} K={K}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=fam)
+    check_gemm(c, ta, tb, A, B, M, N, K)
+
+
+@pytest.mark.parametrize("fam,bk", DMAS)
+def test_dma_infinity_in_last_k_row(device, fam, bk):
+    # B's last k row holds +inf in column 0: C[:, 0] must be +/-inf or nan
+    # exactly where A[:, K-1] makes it so, and every other column finite.
+    M, N, K = 64, 64, 36
+    g = _rng(21, fam)
+    A = np.abs(g.standard_normal((1, M, K))).astype(np.float32) + 0.5
+    B = g.standard_normal((1, K, N)).astype(np.float32)
+    B[0, K - 1, 0] = np.inf
+    say(f"dma inf in last k row fam={fam}")
+    c = gpu_sgemm(0, 0, A, B, M, N, K, kernel=fam)[0]
+    assert np.all(np.isposinf(c[:, 0]))
+    assert np.all(np.isfinite(c[:, 1:]))
+
+
 def test_dma_refuses_unsupported_problems(device):
     import torch
 
     buf = torch.zeros(1 << 20, device="cuda")
     p = buf.data_ptr()
-    say("dma256 refusals")
-    # K not a multiple of 16
-    assert _raw_select(0, 0, 64, 64, 24, p, 24, p, 64, p, DMA) == -2
-    assert "dma256" in capi.last_error()
-    # K a multiple of 16 but not of the 128x128 kernel's K-tile of 32
-    assert _raw_select(0, 0, 64, 64, 48, p, 48, p, 64, p, capi.KERNEL_DMA128) == -2
-    assert "dma128" in capi.last_error()
-    # A misaligned by one float
-    assert _raw_select(0, 0, 64, 64, 32, p + 4, 32, p, 64, p, DMA) == -2
-    assert _raw_select(0, 0, 64, 64, 32, p + 4, 32, p, 64, p, capi.KERNEL_DMA128) == -2
-    # ld not a multiple of 4
-    assert _raw_select(0, 0, 64, 64, 32, p, 33, p, 64, p, DMA) == -2
-    # N (B's contiguous extent) not a multiple of 4
-    assert _raw_select(0, 0, 64, 66, 32, p, 32, p, 66, p, DMA) == -2
+    say("dma refusals")
+    for fam, _ in DMAS:
+        # K not a multiple of 4
+        assert _raw_select(0, 0, 64, 64, 22, p, 24, p, 64, p, fam) == -2
+        assert "direct-to-LDS" in capi.last_error()
+        # A misaligned by one float
+        assert _raw_select(0, 0, 64, 64, 32, p + 4, 32, p, 64, p, fam) == -2
+        # ld not a multiple of 4
+        assert _raw_select(0, 0, 64, 64, 32, p, 33, p, 64, p, fam) == -2
+        # N (B's contiguous extent) not a multiple of 4
+        assert _raw_select(0, 0, 64, 66, 32, p, 32, p, 66, p, fam) == -2
     torch.cuda.synchronize()
 
 
