@@ -217,27 +217,6 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
     const int64_t B = batch, I = in_features, Hd = hidden, Cc = classes;
     const hipStream_t hs = as_stream(stream);
     int st;
-    // Weight-gradient GEMM with the SGD step fused: dW = op(A) op(B) and
-    // W -= lr * dW in the epilogue (the gradient is still written to dW).
-    auto grad_and_step = [&](bool ta, bool tb, int64_t M, int64_t N, int64_t K,
-                             const float* A, int64_t lda, const float* Bm, int64_t ldb,
-                             float* dW, float* W) {
-        fdl::GemmParams p{};
-        p.A = A;
-        p.B = Bm;
-        p.C = dW;
-        p.upd = W;
-        p.lr = lr;
-        p.lda = lda;
-        p.ldb = ldb;
-        p.ldc = N;
-        p.M = (int)M;
-        p.N = (int)N;
-        p.K = (int)K;
-        p.epilogue = fdl::EPI_SGD;
-        return check_hip(fdl::launch_sgemm(p, ta, tb, 1, fdl::GemmKernel::Auto, hs),
-                         "mlp2_train_step weight update failed");
-    };
     // Forward: H = relu(X W1 + b1), logits = H W2 + b2.
     st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Hd, I, X, I, 0, W1, Hd, 0, H, Hd, 0, 1, b1,
                       nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
@@ -259,25 +238,73 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
                        "mlp2_train_step db2 failed");
         if (st) return st;
     }
-    // G1 = (G2 W2^T) masked by H > 0 (NT GEMM, ReLU-gradient epilogue); this
-    // reads W2 before its update below.
-    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, Hd, Cc, G2, Cc, 0, W2, Cc, 0, G1, Hd, 0, 1,
-                      nullptr, H, FDL_EPILOGUE_RELU_GRAD, stream);
+    // The backward pass runs as three grouped launches, each holding two
+    // independent jobs.  Updates are ordered after every read of the old
+    // value: W2 is read by the G1 GEMM (launch 1) and updated in launch 3, W1
+    // is read by the dX GEMM (launch 2) and updated in launch 3.
+    auto gemm_job = [&](bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float* A,
+                        int64_t lda, const float* Bm, int64_t ldb, float* C, int epi,
+                        const float* aux, float* upd) {
+        fdl::GroupJob j;
+        j.kind = fdl::GroupJob::kGemm;
+        j.ta = ta;
+        j.tb = tb;
+        j.p.A = A;
+        j.p.B = Bm;
+        j.p.C = C;
+        j.p.aux = aux;
+        j.p.upd = upd;
+        j.p.lr = lr;
+        j.p.lda = lda;
+        j.p.ldb = ldb;
+        j.p.ldc = N;
+        j.p.M = (int)M;
+        j.p.N = (int)N;
+        j.p.K = (int)K;
+        j.p.epilogue = epi;
+        return j;
+    };
+    // Launch 1: G1 = (G2 W2^T) masked by H > 0 (NT, ReLU-gradient epilogue)
+    // and dW2 = H^T G2 (TN).
+    st = check_hip(fdl::launch_group2(
+                       gemm_job(false, true, B, Hd, Cc, G2, Cc, W2, Cc, G1,
+                                fdl::EPI_RELU_GRAD, H, nullptr),
+                       gemm_job(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2, fdl::EPI_NONE,
+                                nullptr, nullptr),
+                       hs),
+                   "mlp2_train_step G1/dW2 failed");
     if (st) return st;
-    // dW2 = H^T G2 (TN) and W2 -= lr * dW2.
-    st = grad_and_step(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2, W2);
-    if (st) return st;
-    // dX = G1 W1^T (NT), before W1 changes.
+    // Launch 2: dX = G1 W1^T (NT) and db1 = colsum(G1) with b1 -= lr * db1.
+    fdl::GroupJob db1_job;
+    db1_job.kind = fdl::GroupJob::kColsumSgd;
+    db1_job.x = G1;
+    db1_job.out = db1;
+    db1_job.param = b1;
+    db1_job.lr = lr;
+    db1_job.rows = B;
+    db1_job.cols = Hd;
     if (dX) {
-        st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, B, I, Hd, G1, Hd, 0, W1, Hd, 0, dX, I, 0, 1,
-                          nullptr, nullptr, FDL_EPILOGUE_NONE, stream);
-        if (st) return st;
+        st = check_hip(fdl::launch_group2(gemm_job(false, true, B, I, Hd, G1, Hd, W1, Hd, dX,
+                                                   fdl::EPI_NONE, nullptr, nullptr),
+                                          db1_job, hs),
+                       "mlp2_train_step dX/db1 failed");
+    } else {
+        st = check_hip(fdl::launch_colsum_sgd(G1, db1, b1, lr, B, Hd, hs),
+                       "mlp2_train_step db1 failed");
     }
-    // dW1 = X^T G1 (TN) and W1 -= lr * dW1; db1 = colsum(G1) and b1 -= lr * db1.
-    st = grad_and_step(true, false, I, Hd, B, X, I, G1, Hd, dW1, W1);
     if (st) return st;
-    return check_hip(fdl::launch_colsum_sgd(G1, db1, b1, lr, B, Hd, hs),
-                     "mlp2_train_step db1 failed");
+    // Launch 3: dW1 = X^T G1 (TN) with W1 -= lr * dW1 in the epilogue, and
+    // W2 -= lr * dW2.
+    fdl::GroupJob w2_job;
+    w2_job.kind = fdl::GroupJob::kSgd;
+    w2_job.x = dW2;
+    w2_job.param = W2;
+    w2_job.lr = lr;
+    w2_job.rows = Hd * Cc;
+    return check_hip(fdl::launch_group2(gemm_job(true, false, I, Hd, B, X, I, G1, Hd, dW1,
+                                                 fdl::EPI_SGD, nullptr, W1),
+                                        w2_job, hs),
+                     "mlp2_train_step dW1/W2 failed");
 }
 
 }  // extern "C"

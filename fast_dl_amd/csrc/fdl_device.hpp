@@ -1,0 +1,64 @@
+// Device bodies shared by standalone kernels and grouped launches.  Each body
+// takes its block index (and block count) explicitly so that a grouped kernel
+// can run it on a sub-range of its grid.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fdl {
+
+// Column sums of a row-major rows x cols matrix, 32 columns per block and 8
+// row groups per column (256 threads).  Row groups are added in group order,
+// so the result is deterministic.  With `param`, the block also applies
+// param[c] -= lr * sum (the SGD step of a bias).
+constexpr int kColsumCols = 32;
+constexpr int kColsumGroups = 8;
+constexpr int kColsumThreads = kColsumCols * kColsumGroups;
+
+__device__ __forceinline__ void colsum_body(const float* __restrict__ x, float* __restrict__ out,
+                                            float* __restrict__ param, float lr, int64_t rows,
+                                            int64_t cols, int block) {
+#pragma clang fp contract(off)
+    __shared__ float part[kColsumGroups][kColsumCols];
+    const int cl = threadIdx.x % kColsumCols;
+    const int grp = threadIdx.x / kColsumCols;
+    const int64_t c = block * (int64_t)kColsumCols + cl;
+    const int64_t cc = c < cols ? c : cols - 1;  // clamped: loads stay in bounds
+    float s = 0.0f;
+    int64_t r = grp;
+    for (; r + 7 * kColsumGroups < rows; r += 8 * kColsumGroups) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = x[(r + u * kColsumGroups) * cols + cc];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; r < rows; r += kColsumGroups) s += x[r * cols + cc];
+    part[grp][cl] = s;
+    __syncthreads();
+    if (grp == 0 && c < cols) {
+        float t = part[0][cl];
+#pragma unroll
+        for (int g = 1; g < kColsumGroups; ++g) t += part[g][cl];
+        out[c] = t;
+        if (param) {
+            const float step = lr * t;
+            param[c] = param[c] - step;
+        }
+    }
+}
+
+// p[i] -= lr * g[i] over a grid-stride range; the product is rounded before
+// the subtraction (no FMA contraction), as in the reference's host update.
+__device__ __forceinline__ void sgd_body(float* __restrict__ p, const float* __restrict__ g,
+                                         float lr, int64_t n, int block, int nblocks) {
+#pragma clang fp contract(off)
+    for (int64_t idx = block * (int64_t)blockDim.x + threadIdx.x; idx < n;
+         idx += (int64_t)nblocks * blockDim.x) {
+        p[idx] -= lr * g[idx];
+    }
+}
+
+}  // namespace fdl

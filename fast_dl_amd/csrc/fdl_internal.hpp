@@ -59,6 +59,26 @@ enum class GemmKernel : int {
 bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
                    int64_t batch);
 
+// One job of a grouped launch (launch_group2): a split-K GEMM (32x32 output
+// tiles, four waves per block, any epilogue), a column sum with the bias SGD
+// step, or an SGD update p -= lr * g.
+struct GroupJob {
+    enum Kind { kGemm, kColsumSgd, kSgd };
+    Kind kind = kGemm;
+    GemmParams p{};              // kGemm
+    bool ta = false, tb = false;
+    const float* x = nullptr;    // kColsumSgd: rows x cols input; kSgd: gradient
+    float* out = nullptr;        // kColsumSgd: column sums
+    float* param = nullptr;      // kColsumSgd, kSgd: the parameter updated
+    float lr = 0.0f;
+    int64_t rows = 0, cols = 0;  // kSgd: rows is the element count
+};
+
+// Runs two independent jobs in one launch, job 0 on the first blocks of the
+// grid.  Supported pairs are the ones the MLP step uses: (NT GEMM, TN GEMM),
+// (NT GEMM, column sum), (TN GEMM, SGD); others return hipErrorInvalidValue.
+hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream);
+
 // Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
 hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,
                         int64_t batch, GemmKernel kernel, hipStream_t stream);

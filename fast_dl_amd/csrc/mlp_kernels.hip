@@ -2,6 +2,7 @@
 // column sums, row softmax, softmax cross-entropy (loss and gradient), SGD
 // and the Philox random fills.  All are HBM- or latency-bound; none uses
 // atomics, so every result is deterministic run to run.
+#include "fdl_device.hpp"
 #include "fdl_internal.hpp"
 
 #include <algorithm>
@@ -46,44 +47,10 @@ __global__ void relu_backward_kernel(const float* __restrict__ g,
     }
 }
 
-// Column sums.  A block owns 32 columns; its 8 row groups each add every 8th
-// row (unrolled so eight independent loads are in flight per thread), and the
-// 8 group partials are added in group order: deterministic run to run.
-// With `param`, the block also applies param[c] -= lr * sum (SGD on a bias).
-constexpr int kColsumCols = 32;
-constexpr int kColsumGroups = 8;
-
-__global__ void __launch_bounds__(kColsumCols * kColsumGroups)
+__global__ void __launch_bounds__(kColsumThreads)
 colsum_kernel(const float* __restrict__ x, float* __restrict__ out,
               float* __restrict__ param, float lr, int64_t rows, int64_t cols) {
-#pragma clang fp contract(off)
-    __shared__ float part[kColsumGroups][kColsumCols];
-    const int cl = threadIdx.x % kColsumCols;
-    const int grp = threadIdx.x / kColsumCols;
-    const int64_t c = blockIdx.x * (int64_t)kColsumCols + cl;
-    const int64_t cc = c < cols ? c : cols - 1;  // clamped: loads stay in bounds
-    float s = 0.0f;
-    int64_t r = grp;
-    for (; r + 7 * kColsumGroups < rows; r += 8 * kColsumGroups) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = x[(r + u * kColsumGroups) * cols + cc];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
-    }
-    for (; r < rows; r += kColsumGroups) s += x[r * cols + cc];
-    part[grp][cl] = s;
-    __syncthreads();
-    if (grp == 0 && c < cols) {
-        float t = part[0][cl];
-#pragma unroll
-        for (int g = 1; g < kColsumGroups; ++g) t += part[g][cl];
-        out[c] = t;
-        if (param) {
-            const float step = lr * t;
-            param[c] = param[c] - step;
-        }
-    }
+    colsum_body(x, out, param, lr, rows, cols, blockIdx.x);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -153,8 +120,6 @@ softmax_xent_kernel(const float* __restrict__ logits,
     if (threadIdx.x == 0 && loss) loss[0] = part[0];
 }
 
-// p -= lr * g with the product rounded before the subtraction (no FMA
-// contraction), as the reference's x86 host update computes it.
 // Softmax cross-entropy for classes <= kXentFusedMaxClasses with the bias
 // gradient and the bias SGD step fused: one block walks the batch in chunks of
 // 256 rows staged through LDS with coalesced loads (thread t owns row t of
@@ -170,8 +135,12 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
 #pragma clang fp contract(off)
     __shared__ float zs[kBlock * kXentFusedMaxClasses];
     __shared__ float part[kBlock];
+    __shared__ float wpart[kBlock / 64];
     const int t = threadIdx.x;
     const float inv_b = 1.0f / (float)batch;
+    // Loads whose values are needed late are issued first, so the step pays
+    // one global-memory round trip, not one per phase.
+    const float bold = t < classes ? bparam[t] : 0.0f;
     float lsum = 0.0f;
     // Column sums of the gradient: thread t adds class cls over the rows
     // r = grp, grp + ngrp, ... of each chunk (ngrp groups of cpad threads).
@@ -183,6 +152,7 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
     for (int64_t r0 = 0; r0 < batch; r0 += kBlock) {
         const int rows = (int)min<int64_t>(kBlock, batch - r0);
         const int n = rows * (int)classes;
+        const int64_t label = t < rows ? labels[r0 + t] : -1;
         const float* zsrc = logits + r0 * classes;
         for (int e = t; e < n; e += kBlock) zs[e] = zsrc[e];
         __syncthreads();
@@ -192,7 +162,6 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
             for (int c = 1; c < classes; ++c) mx = fmaxf(mx, z[c]);
             float s = 0.0f;
             for (int c = 0; c < classes; ++c) s += expf(z[c] - mx);
-            const int64_t label = labels[r0 + t];
             const bool valid = label >= 0 && label < classes;
             if (valid) lsum += (logf(s) + mx - z[label]) * inv_b;
             const float inv_s = 1.0f / s;
@@ -210,33 +179,31 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
         }
         __syncthreads();
     }
-    // Group partials of each class, added in group order.
+    // Group partials of each class, added in group order; the loss is summed
+    // within each wave, then over the waves in wave order.
     part[t] = dbc;
+    lsum = wave_sum(lsum);
+    if ((t & 63) == 0) wpart[t >> 6] = lsum;
     __syncthreads();
     if (t < classes) {
         float d = part[t];
         for (int g = 1; g < ngrp; ++g) d += part[g * cpad + t];
         db[t] = d;
         const float step = lr * d;
-        bparam[t] = bparam[t] - step;
+        bparam[t] = bold - step;
     }
-    __syncthreads();
-    part[t] = lsum;
-    __syncthreads();
-    for (int w = kBlock / 2; w > 0; w >>= 1) {
-        if (t < w) part[t] += part[t + w];
-        __syncthreads();
+    if (t == 0 && loss) {
+        float l = wpart[0];
+        for (int w = 1; w < kBlock / 64; ++w) l += wpart[w];
+        loss[0] = l;
     }
-    if (t == 0 && loss) loss[0] = part[0];
 }
 
+// p -= lr * g with the product rounded before the subtraction (no FMA
+// contraction), as the reference's x86 host update computes it.
 __global__ void sgd_kernel(float* __restrict__ p, const float* __restrict__ g,
                            float lr, int64_t n) {
-#pragma clang fp contract(off)
-    for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < n;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-        p[idx] -= lr * g[idx];
-    }
+    sgd_body(p, g, lr, n, blockIdx.x, gridDim.x);
 }
 
 struct SgdMulti {
@@ -347,7 +314,7 @@ hipError_t launch_colsum_sgd(const float* x, float* out, float* param, float lr,
                              int64_t rows, int64_t cols, hipStream_t stream) {
     if (cols == 0) return hipSuccess;
     const unsigned blocks = (unsigned)((cols + kColsumCols - 1) / kColsumCols);
-    hipLaunchKernelGGL(colsum_kernel, dim3(blocks), dim3(kColsumCols * kColsumGroups), 0,
+    hipLaunchKernelGGL(colsum_kernel, dim3(blocks), dim3(kColsumThreads), 0,
                        stream, x, out, param, lr, rows, cols);
     return hipGetLastError();
 }

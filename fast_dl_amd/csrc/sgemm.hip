@@ -9,6 +9,7 @@
 //   operand b: lane l supplies B[kk = l / 32][j = l % 32]
 //   result   : lane l, register r holds D[i][j] with j = l % 32 and
 //              i = 8 * (r / 4) + 4 * (l / 32) + (r % 4)
+#include "fdl_device.hpp"
 #include "fdl_internal.hpp"
 
 #include <algorithm>
@@ -63,6 +64,55 @@ __device__ __forceinline__ void store_epilogue(float v, const GemmParams& p,
         case EPI_SGD: {
             const float step = p.lr * v;
             upd[off] = upd[off] - step;
+            break;
+        }
+        default:
+            break;
+    }
+    C[off] = v;
+}
+
+// The operand an epilogue reads besides the accumulator (bias[j], aux[off] or
+// upd[off]), loaded before the K loop so its latency overlaps the MFMAs.
+__device__ __forceinline__ float epilogue_operand(const GemmParams& p,
+                                                  const float* __restrict__ aux,
+                                                  const float* __restrict__ upd, int64_t off,
+                                                  int j) {
+    switch (p.epilogue) {
+        case EPI_BIAS:
+        case EPI_BIAS_RELU:
+            return p.bias[j];
+        case EPI_RELU_GRAD:
+            return aux[off];
+        case EPI_SGD:
+            return upd[off];
+        default:
+            return 0.0f;
+    }
+}
+
+// store_epilogue with the extra operand already loaded (epilogue_operand).
+__device__ __forceinline__ void store_epilogue_pre(float v, const GemmParams& p,
+                                                   float* __restrict__ C,
+                                                   float* __restrict__ upd, int64_t off,
+                                                   float pre) {
+#pragma clang fp contract(off)
+    switch (p.epilogue) {
+        case EPI_BIAS:
+            v = v + pre;
+            break;
+        case EPI_BIAS_RELU:
+            v = fmaxf(0.0f, v + pre);
+            break;
+        case EPI_RELU:
+            v = fmaxf(0.0f, v);
+            break;
+        case EPI_RELU_GRAD:
+            v = pre > 0.0f ? v : 0.0f;
+            break;
+        case EPI_SGD: {
+            const float step = p.lr * v;
+            upd[off] = pre - step;
             break;
         }
         default:
@@ -772,9 +822,12 @@ __device__ __forceinline__ void splitk_load_group(const float* __restrict__ A,
     }
 }
 
+// The body takes its block index and the number of blocks that share the
+// tile mapping explicitly, so a grouped launch can run it on a sub-range of
+// its grid (sgemm_group_kernel).
 template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
-__global__ void __launch_bounds__(KW * 64)
-sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
+__device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, int tiles_n,
+                                              int kchunk, int bid, int nblocks, int64_t bz) {
     __shared__ float red[KW][16][kWave];
 
     const int tid = threadIdx.x;
@@ -784,10 +837,9 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     const int h = lane >> 5;
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(bid, nblocks, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * 32;
     const int n0 = tn * 32;
-    const int64_t bz = blockIdx.y;
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
 
@@ -799,6 +851,25 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     const int kend = min(p.K, kbeg + kchunk);
     const int groups = kend > kbeg ? (kend - kbeg + 7) / 8 : 0;
     const int supers = (groups + ITS - 1) / ITS;
+
+    float* __restrict__ C = p.C + bz * p.strideC;
+    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+    // The epilogue's elements of this thread, and their extra operand,
+    // fetched now (see epilogue_operand).
+    constexpr int kEpi = (16 * kWave + KW * kWave - 1) / (KW * kWave);
+    float pre[kEpi];
+#pragma unroll
+    for (int q = 0; q < kEpi; ++q) {
+        const int e = tid + q * KW * kWave;
+        const int r = e / kWave;
+        const int ln = e % kWave;
+        const int gi = m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+        const int gj = n0 + (ln & 31);
+        pre[q] = (e < 16 * kWave && gi < p.M && gj < p.N)
+                     ? epilogue_operand(p, aux, upd, (int64_t)gi * p.ldc + gj, gj)
+                     : 0.0f;
+    }
 
     floatx16 acc;
 #pragma unroll
@@ -843,10 +914,10 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
 
-    float* __restrict__ C = p.C + bz * p.strideC;
-    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
-    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
-    for (int e = tid; e < 16 * kWave; e += KW * kWave) {
+#pragma unroll
+    for (int q = 0; q < kEpi; ++q) {
+        const int e = tid + q * KW * kWave;
+        if (e >= 16 * kWave) break;
         const int r = e / kWave;
         const int ln = e % kWave;
         float v = 0.0f;
@@ -855,10 +926,16 @@ sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
         const int gi = m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
         const int gj = n0 + (ln & 31);
         if (gi < p.M && gj < p.N) {
-            const int64_t off = (int64_t)gi * p.ldc + gj;
-            store_epilogue(v, p, C, aux, upd, off, gj);
+            store_epilogue_pre(v, p, C, upd, (int64_t)gi * p.ldc + gj, pre[q]);
         }
     }
+}
+
+template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(KW * 64)
+sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
+    splitk32_body<KW, ITS, TA, TB, VA, VB>(p, tiles_m, tiles_n, kchunk, blockIdx.x, gridDim.x,
+                                           blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -900,6 +977,25 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     const int64_t bz = blockIdx.y;
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
+
+    float* __restrict__ C = p.C + bz * p.strideC;
+    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+    // The epilogue's elements of this thread and their extra operand, fetched
+    // now (see epilogue_operand).
+    constexpr int kEpi = (4 * kWave + KW * kWave - 1) / (KW * kWave);
+    float pre[kEpi];
+#pragma unroll
+    for (int u = 0; u < kEpi; ++u) {
+        const int e = tid + u * KW * kWave;
+        const int r = e / kWave;
+        const int ln = e % kWave;
+        const int gi = m0 + 4 * (ln >> 4) + r;
+        const int gj = n0 + (ln & 15);
+        pre[u] = (e < 4 * kWave && gi < p.M && gj < p.N)
+                     ? epilogue_operand(p, aux, upd, (int64_t)gi * p.ldc + gj, gj)
+                     : 0.0f;
+    }
 
     const int row = min(m0 + i, p.M - 1);
     const int col = min(n0 + i, p.N - 1);
@@ -946,10 +1042,10 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
     for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
 
-    float* __restrict__ C = p.C + bz * p.strideC;
-    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
-    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
-    for (int e = tid; e < 4 * kWave; e += KW * kWave) {
+#pragma unroll
+    for (int u = 0; u < kEpi; ++u) {
+        const int e = tid + u * KW * kWave;
+        if (e >= 4 * kWave) break;
         const int r = e / kWave;
         const int ln = e % kWave;
         float v = 0.0f;
@@ -958,8 +1054,7 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
         const int gi = m0 + 4 * (ln >> 4) + r;
         const int gj = n0 + (ln & 15);
         if (gi < p.M && gj < p.N) {
-            const int64_t off = (int64_t)gi * p.ldc + gj;
-            store_epilogue(v, p, C, aux, upd, off, gj);
+            store_epilogue_pre(v, p, C, upd, (int64_t)gi * p.ldc + gj, pre[u]);
         }
     }
 }
@@ -1178,6 +1273,54 @@ hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
     }
 #undef FDL_SPLITK_CASE
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped launches: two independent jobs in one grid, so that dependent
+// chains of small kernels (the MLP step's backward pass) pay one launch for
+// two jobs.  Every job body runs on 256 threads.
+// ---------------------------------------------------------------------------
+struct GroupDev {
+    GemmParams p;
+    int tiles_m, tiles_n, kchunk, blocks;
+    const float* x;
+    float* out;
+    float* param;
+    float lr;
+    int64_t rows, cols;
+};
+
+constexpr int kGroupKW = 4;   // split-K waves of a grouped GEMM job (256 threads)
+constexpr int kGroupITS = 2;
+
+template <bool TA, bool TB, bool VA, bool VB>
+struct JobGemm {
+    static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
+        splitk32_body<kGroupKW, kGroupITS, TA, TB, VA, VB>(a.p, a.tiles_m, a.tiles_n, a.kchunk,
+                                                           bid, a.blocks, 0);
+    }
+};
+
+struct JobColsumSgd {
+    static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
+        colsum_body(a.x, a.out, a.param, a.lr, a.rows, a.cols, bid);
+    }
+};
+
+struct JobSgd {
+    static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
+        sgd_body(a.param, a.x, a.lr, a.rows, bid, a.blocks);
+    }
+};
+
+template <class J0, class J1>
+__global__ void __launch_bounds__(kGroupKW * kWave)
+sgemm_group_kernel(GroupDev a0, GroupDev a1) {
+    if ((int)blockIdx.x < a0.blocks) {
+        J0::run(a0, blockIdx.x);
+    } else {
+        J1::run(a1, (int)blockIdx.x - a0.blocks);
+    }
 }
 
 template <int KW, int ITS = 1>
@@ -1403,6 +1546,80 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
         }
     }
     return best;
+}
+
+namespace {
+
+GroupDev group_dev(const GroupJob& j) {
+    GroupDev d{};
+    d.p = j.p;
+    d.x = j.x;
+    d.out = j.out;
+    d.param = j.param;
+    d.lr = j.lr;
+    d.rows = j.rows;
+    d.cols = j.cols;
+    switch (j.kind) {
+        case GroupJob::kGemm: {
+            d.tiles_m = (j.p.M + 31) / 32;
+            d.tiles_n = (j.p.N + 31) / 32;
+            constexpr int kSuper = 8 * kGroupITS;
+            int kchunk = (j.p.K + kGroupKW - 1) / kGroupKW;
+            d.kchunk = std::max(kSuper, (kchunk + kSuper - 1) / kSuper * kSuper);
+            d.blocks = d.tiles_m * d.tiles_n;
+            break;
+        }
+        case GroupJob::kColsumSgd:
+            d.blocks = (int)((j.cols + kColsumCols - 1) / kColsumCols);
+            break;
+        case GroupJob::kSgd:
+            d.blocks = (int)std::min<int64_t>((j.rows + 4 * 256 - 1) / (4 * 256), 1024);
+            break;
+    }
+    return d;
+}
+
+template <class J0, class J1>
+hipError_t launch_group_pair(const GroupDev& a0, const GroupDev& a1, hipStream_t stream) {
+    hipLaunchKernelGGL((sgemm_group_kernel<J0, J1>), dim3(a0.blocks + a1.blocks),
+                       dim3(kGroupKW * kWave), 0, stream, a0, a1);
+    return hipGetLastError();
+}
+
+// Vector flags of an NT GEMM job (A and B both k-contiguous), as launch_sgemm
+// derives them.
+template <class J1>
+hipError_t launch_nt_then(const GroupJob& j0, const GroupDev& a0, const GroupDev& a1,
+                          hipStream_t stream) {
+    const bool va = vec_ok(j0.p.A, j0.p.K, j0.p.lda, j0.p.strideA, 1);
+    const bool vb = vec_ok(j0.p.B, j0.p.K, j0.p.ldb, j0.p.strideB, 1);
+    if (va && vb) return launch_group_pair<JobGemm<false, true, true, true>, J1>(a0, a1, stream);
+    if (va) return launch_group_pair<JobGemm<false, true, true, false>, J1>(a0, a1, stream);
+    if (vb) return launch_group_pair<JobGemm<false, true, false, true>, J1>(a0, a1, stream);
+    return launch_group_pair<JobGemm<false, true, false, false>, J1>(a0, a1, stream);
+}
+
+}  // namespace
+
+hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream) {
+    const bool nt0 = j0.kind == GroupJob::kGemm && !j0.ta && j0.tb;
+    const bool tn0 = j0.kind == GroupJob::kGemm && j0.ta && !j0.tb;
+    const bool tn1 = j1.kind == GroupJob::kGemm && j1.ta && !j1.tb;
+    for (const GroupJob* j : {&j0, &j1}) {
+        if (j->kind == GroupJob::kGemm && (j->p.M <= 0 || j->p.N <= 0 || j->p.K <= 0)) {
+            return hipErrorInvalidValue;
+        }
+    }
+    const GroupDev a0 = group_dev(j0);
+    const GroupDev a1 = group_dev(j1);
+    if (nt0 && tn1) return launch_nt_then<JobGemm<true, false, false, false>>(j0, a0, a1, stream);
+    if (nt0 && j1.kind == GroupJob::kColsumSgd) {
+        return launch_nt_then<JobColsumSgd>(j0, a0, a1, stream);
+    }
+    if (tn0 && j1.kind == GroupJob::kSgd) {
+        return launch_group_pair<JobGemm<true, false, false, false>, JobSgd>(a0, a1, stream);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,

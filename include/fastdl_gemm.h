@@ -218,7 +218,7 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels,
 
 /*
  * The same training step captured once into a HIP graph and replayed: one
- * launch per step instead of eight, for loops that keep the same buffers
+ * launch per step instead of six, for loops that keep the same buffers
  * (refill X and labels in place between steps).  create captures
  * fdl_mlp2_train_step with these exact pointers on `stream` (a temporary
  * stream when NULL) and instantiates it; launch replays it on `stream`;
