@@ -19,6 +19,9 @@ const char* to_string(GemmAlgo algo) {
         case GemmAlgo::MfmaTiled64: return "mfma_tiled64";
         case GemmAlgo::MfmaSplitK: return "mfma_splitk32";
         case GemmAlgo::Skinny: return "skinny";
+        case GemmAlgo::MfmaDma256: return "mfma_dma256";
+        case GemmAlgo::MfmaDma128: return "mfma_dma128";
+        case GemmAlgo::MfmaDma64: return "mfma_dma64";
     }
     return "unknown";
 }
@@ -32,6 +35,9 @@ int kernel_id(GemmAlgo algo) {
         case GemmAlgo::MfmaTiled64: return FDL_KERNEL_TILED64;
         case GemmAlgo::MfmaSplitK: return FDL_KERNEL_SPLITK32;
         case GemmAlgo::Skinny: return FDL_KERNEL_SKINNY;
+        case GemmAlgo::MfmaDma256: return FDL_KERNEL_DMA256;
+        case GemmAlgo::MfmaDma128: return FDL_KERNEL_DMA128;
+        case GemmAlgo::MfmaDma64: return FDL_KERNEL_DMA64;
     }
     return FDL_KERNEL_AUTO;
 }

@@ -17,6 +17,10 @@ enum class GemmAlgo {
     MfmaTiled64,    // 64x64x16 LDS double-buffered fp32 MFMA tile
     MfmaSplitK,     // 32x32 MFMA tile, K split over the waves of a block
     Skinny,         // VALU streaming kernel for m <= 8
+    MfmaDma256,     // 256x256x16 tile fed by direct global->LDS copies (k % 4 == 0,
+                    // 16-byte-aligned operands; std::runtime_error otherwise)
+    MfmaDma128,     // 128x128x32 tile, same copies, two blocks per CU
+    MfmaDma64,      // 64x64x64 tile, same copies, for mid-size problems
 };
 
 const char* to_string(GemmAlgo algo);

@@ -129,6 +129,41 @@ int main() {
         return true;
     });
 
+    run("matmul_direct_to_lds_algos", [] {
+        // k and n multiples of 4: the direct-to-LDS kernels accept the shape;
+        // k = 100 leaves a partial last K-tile for all three tiles.
+        const int m = 300, n = 136, k = 100;
+        auto a = randv(m * k, 11), b = randv(k * n, 12);
+        auto want = host_gemm(a, b, m, n, k);
+        auto ta = dl::Tensor::from_host<float>(a, dl::Shape({m, k}), kDev);
+        auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
+        for (auto algo : {dl::kernels::GemmAlgo::MfmaDma256, dl::kernels::GemmAlgo::MfmaDma128,
+                          dl::kernels::GemmAlgo::MfmaDma64}) {
+            dl::Tensor tc(dl::Shape({m, n}), dl::DType::Float32, kDev);
+            dl::kernels::gemm(static_cast<const float*>(ta.data()),
+                              static_cast<const float*>(tb.data()), static_cast<float*>(tc.data()),
+                              m, n, k, algo);
+            if (!close(tc.to_host<float>(), want, 1e-5f)) {
+                std::cout << "  algo " << dl::kernels::to_string(algo) << " mismatch" << std::endl;
+                return false;
+            }
+        }
+        // k % 4 != 0: a forced direct-to-LDS kernel is refused with an exception.
+        const int k2 = 50;
+        auto a2 = dl::Tensor::from_host<float>(randv(m * k2, 13), dl::Shape({m, k2}), kDev);
+        auto b2 = dl::Tensor::from_host<float>(randv(k2 * n, 14), dl::Shape({k2, n}), kDev);
+        dl::Tensor c2(dl::Shape({m, n}), dl::DType::Float32, kDev);
+        try {
+            dl::kernels::gemm(static_cast<const float*>(a2.data()),
+                              static_cast<const float*>(b2.data()), static_cast<float*>(c2.data()),
+                              m, n, k2, dl::kernels::GemmAlgo::MfmaDma128);
+        } catch (const std::runtime_error&) {
+            return true;
+        }
+        std::cout << "  k % 4 != 0 was not refused" << std::endl;
+        return false;
+    });
+
     run("linear_backward", [] {
         const int rows = 33, in = 20, out = 7;
         auto x = randv(rows * in, 3), w = randv(in * out, 4), g = randv(rows * out, 5);
