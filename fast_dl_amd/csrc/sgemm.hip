@@ -13,6 +13,8 @@
 #include "fdl_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 namespace fdl {
 
@@ -494,7 +496,9 @@ struct DmaOperand {
 
     __device__ __forceinline__ void init(int64_t ld, int mn0, int mn_lim, int tid) {
         const int lane = tid & (kWave - 1);
-        const int wave = tid / kWave;
+        // Wave-uniform by construction; readfirstlane lets the compiler keep
+        // loff in scalar registers, so each copy sets M0 without a VALU step.
+        const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int ins = wave * PER + i;
@@ -520,11 +524,22 @@ struct DmaOperand {
     __device__ __forceinline__ void issue(const float* __restrict__ base, int64_t ld, int k0,
                                           int K, float* stage, int tid) const {
         if (k0 + BK <= K) {
-            const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) dma_copy16(base + goff[i] + koff, stage + loff[i]);
-            return;
+            issue_full(base, ld, k0, stage);
+        } else {
+            issue_tail(base, ld, k0, K, stage, tid);
         }
+    }
+
+    // A tile wholly inside K: no per-copy bounds work.
+    __device__ __forceinline__ void issue_full(const float* __restrict__ base, int64_t ld, int k0,
+                                               float* stage) const {
+        const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) dma_copy16(base + goff[i] + koff, stage + loff[i]);
+    }
+
+    __device__ __forceinline__ void issue_tail(const float* __restrict__ base, int64_t ld, int k0,
+                                               int K, float* stage, int tid) const {
         const int lane = tid & (kWave - 1);
         const int wave = tid / kWave;
 #pragma unroll
@@ -556,6 +571,23 @@ struct DmaOperand {
         }
     }
 };
+
+// Scheduling hint for one MFMA group: after MFMA j, the reads and copies
+// that bring the running totals to ceil(total * (j + 1) / kMfma), so both are
+// spread evenly over the group (the builtin needs constant counts).
+template <int kMfma, int kReads, int kCopies, int J>
+__device__ __forceinline__ void spread_hint_one() {
+    constexpr int r = (kReads * (J + 1) + kMfma - 1) / kMfma - (kReads * J + kMfma - 1) / kMfma;
+    constexpr int c = (kCopies * (J + 1) + kMfma - 1) / kMfma - (kCopies * J + kMfma - 1) / kMfma;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);  // DS reads
+    if constexpr (c > 0) __builtin_amdgcn_sched_group_barrier(0x010, c, 0);  // VMEM
+}
+
+template <int kMfma, int kReads, int kCopies, int... J>
+__device__ __forceinline__ void spread_hint(std::integer_sequence<int, J...>) {
+    (spread_hint_one<kMfma, kReads, kCopies, J>(), ...);
+}
 
 template <class Cfg, bool TA, bool TB>
 __global__ void __launch_bounds__(Cfg::NT)
@@ -615,11 +647,14 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
 
     float a[2][4][FM];
     float b[2][4][FN];
-    // Reads group g of tile `tile` into register slot `slot`; in the tile
-    // that crosses K, A and B values at k >= K are zeroed (the LDS slots past
-    // K hold redirected copies of valid data; zeroing both keeps an infinity
-    // there from turning into 0 * inf).
-    auto read_group = [&](const float* as, const float* bs, int g, int slot, int tile) {
+    // Reads group g of tile `tile` into register slot `slot`.  `masked` (a
+    // compile-time flag, so the steady-state loop has no branch between the
+    // reads and the MFMAs) marks the tile that crosses K: there A and B
+    // values at k >= K are zeroed (the LDS slots past K hold redirected copies
+    // of valid data; zeroing both keeps an infinity there from turning into
+    // 0 * inf).
+    auto read_group = [&](const float* as, const float* bs, int g, int slot, int tile,
+                          auto masked) __attribute__((always_inline)) {
         float v[4];
 #pragma unroll
         for (int mi = 0; mi < FM; ++mi) {
@@ -633,7 +668,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) b[slot][q][ni] = v[q];
         }
-        if (tile == tail_tile) {
+        if constexpr (decltype(masked)::value) {
             const int kbase = tile * BK + 8 * g + 4 * half;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -647,7 +682,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         }
     };
 
-    auto mfma_group = [&](int slot) {
+    auto mfma_group = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -674,6 +709,14 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
                 __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPer * kPairs, 0);
         }
     };
+    // The same for the group that also issues the next tile's copies: after
+    // each MFMA, an even share of the fragment reads (DS) and copies (VMEM).
+    auto interleave_hint_copies = [&]() {
+        if (Cfg::ILV) {
+            constexpr int kMfma = 4 * FM * FN;
+            spread_hint<kMfma, FM + 2 * FN, PER_TILE>(std::make_integer_sequence<int, kMfma>{});
+        }
+    };
 
     if constexpr (Cfg::XPIPE != 0) {
         // Cross-tile pipeline (two stages): the barrier sits before the last
@@ -682,6 +725,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         // (lgkmcnt 0) and tile t+1 has landed (vmcnt 0: it is the only copy in
         // flight), so tile t+2 can go into tile t's stage right after it.
         static_assert(S == 2 && NG % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
+        using No = std::false_type;
+        using Yes = std::true_type;
+        const bool has_tail = tail_tile >= 0;
         if (ktiles > 1) {
             issue_tile(1, 1);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_TILE));
@@ -691,15 +737,59 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        read_group(As, Bs, 0, 0, 0);
-        for (int t = 0; t < ktiles; ++t) {
+        if (tail_tile == 0) {
+            read_group(As, Bs, 0, 0, 0, Yes{});
+        } else {
+            read_group(As, Bs, 0, 0, 0, No{});
+        }
+        // One K-tile of the steady state (tiles t+1 and t+2 exist and are
+        // wholly inside K).  Nothing here branches, so each group's fragment
+        // reads stay in one scheduling region with the MFMAs they are
+        // interleaved with.
+        auto ktile_steady = [&](int t) __attribute__((always_inline)) {
             const int cur = t & 1;
             const float* as = As + cur * OpA::STAGE;
             const float* bs = Bs + cur * OpB::STAGE;
 #pragma unroll
             for (int g = 0; g + 1 < NG; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                read_group(as, bs, g + 1, (g + 1) & 1, t);
+                read_group(as, bs, g + 1, (g + 1) & 1, t, No{});
+                mfma_group(g & 1);
+                interleave_hint();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // vmcnt(0) lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            // The copies of tile t+2 (into the stage every wave has finished
+            // reading) and the first reads of tile t+1 are spread between the
+            // last group's MFMAs.
+            opa.issue_full(A, p.lda, (t + 2) * BK, As + cur * OpA::STAGE);
+            opb.issue_full(B, p.ldb, (t + 2) * BK, Bs + cur * OpB::STAGE);
+            read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1, No{});
+            mfma_group((NG - 1) & 1);
+            interleave_hint_copies();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // The last tiles (up to three), with run-time checks for the tile
+        // that crosses K and for the end of K.
+        auto read_rt = [&](const float* as, const float* bs, int g, int slot, int tile) {
+            if (tile == tail_tile) {
+                read_group(as, bs, g, slot, tile, Yes{});
+            } else {
+                read_group(as, bs, g, slot, tile, No{});
+            }
+        };
+        auto ktile_last = [&](int t) {
+            const int cur = t & 1;
+            const float* as = As + cur * OpA::STAGE;
+            const float* bs = Bs + cur * OpB::STAGE;
+#pragma unroll
+            for (int g = 0; g + 1 < NG; ++g) {
+                __builtin_amdgcn_sched_barrier(0);
+                read_rt(as, bs, g + 1, (g + 1) & 1, t);
                 mfma_group(g & 1);
                 interleave_hint();
                 __builtin_amdgcn_sched_barrier(0);
@@ -711,12 +801,18 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             if (t + 2 < ktiles) issue_tile(t + 2, cur);
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < ktiles) {
-                read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1);
+                read_rt(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1);
             }
             mfma_group((NG - 1) & 1);
             interleave_hint();
             __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        // Steady state while tile t+2 is not the last tile; a K that ends in
+        // a full tile needs no checks until its last two tiles.
+        const int steady = has_tail ? ktiles - 3 : ktiles - 2;
+        int t = 0;
+        for (; t < steady; ++t) ktile_steady(t);
+        for (; t < ktiles; ++t) ktile_last(t);
     } else {
         int stage = 0;
         for (int t = 0; t < ktiles; ++t) {
@@ -737,11 +833,19 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             }
             const float* as = As + stage * OpA::STAGE;
             const float* bs = Bs + stage * OpB::STAGE;
-            read_group(as, bs, 0, 0, t);
+            // This path (three or more stages) masks at run time.
+            auto read_rt = [&](int g, int slot) {
+                if (t == tail_tile) {
+                    read_group(as, bs, g, slot, t, std::true_type{});
+                } else {
+                    read_group(as, bs, g, slot, t, std::false_type{});
+                }
+            };
+            read_rt(0, 0);
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                if (g + 1 < NG) read_group(as, bs, g + 1, (g + 1) & 1, t);
+                if (g + 1 < NG) read_rt(g + 1, (g + 1) & 1);
                 if (!Cfg::ILV) __builtin_amdgcn_sched_barrier(0);
                 mfma_group(g & 1);
                 if (g + 1 < NG) interleave_hint();
@@ -1445,8 +1549,8 @@ struct TileModel {
 
 constexpr TileModel kTileModels[] = {
     {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f}},
-    {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.67f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f, 0.82f}},
-    {GemmKernel::Dma64, 64, 64, 2, 4, {0, 0.46f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f, 0.66f}},
+    {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.75f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f}},
+    {GemmKernel::Dma64, 64, 64, 2, 4, {0, 0.535f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f}},
     {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.66f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f}},

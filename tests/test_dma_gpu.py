@@ -85,11 +85,14 @@ def _raw_select(ta, tb, M, N, K, a_ptr, lda, b_ptr, ldb, c_ptr, kernel):
 
 @pytest.mark.parametrize("fam,bk", DMAS)
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
-@pytest.mark.parametrize("K", [4, 20, 100, 1000])
+@pytest.mark.parametrize("K", [4, 20, 36, 52, 68, 100, 132, 196, 1000])
 def test_dma_partial_last_k_tile(device, fam, bk, ta, tb, K):
     # K a multiple of 4 but not of the K-tile: the last tile's copies past K
     # are redirected and masked.  Non-finite values right at the end of K in
-    # the other operand must not leak into the masked slots as 0 * inf.
+    # the other operand must not leak into the masked slots as 0 * inf.  The
+    # K values give 1 to 5 K-tiles with a partial last one for each tile
+    # depth (16, 32, 64), so the pipelined loop runs zero, one and several
+    # steady-state tiles before its checked last tiles.
     M, N = 132, 200
     A, B = operands(_rng(K, ta, tb, fam), ta, tb, M, N, K, 1)
     say(f"dma partial K-tile fam={fam} ta={ta} tb={tb} K={K}")
