@@ -16,6 +16,7 @@ from .capi import (  # noqa: F401
     EPILOGUE_RELU_GRAD,
     KERNEL_AUTO,
     KERNEL_DMA64,
+    KERNEL_DMA128W8,
     KERNEL_DMA128,
     KERNEL_DMA256,
     KERNEL_SKINNY,

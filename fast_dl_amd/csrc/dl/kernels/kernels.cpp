@@ -22,6 +22,7 @@ const char* to_string(GemmAlgo algo) {
         case GemmAlgo::MfmaDma256: return "mfma_dma256";
         case GemmAlgo::MfmaDma128: return "mfma_dma128";
         case GemmAlgo::MfmaDma64: return "mfma_dma64";
+        case GemmAlgo::MfmaDma128W8: return "mfma_dma128w8";
     }
     return "unknown";
 }
@@ -38,6 +39,7 @@ int kernel_id(GemmAlgo algo) {
         case GemmAlgo::MfmaDma256: return FDL_KERNEL_DMA256;
         case GemmAlgo::MfmaDma128: return FDL_KERNEL_DMA128;
         case GemmAlgo::MfmaDma64: return FDL_KERNEL_DMA64;
+        case GemmAlgo::MfmaDma128W8: return FDL_KERNEL_DMA128W8;
     }
     return FDL_KERNEL_AUTO;
 }

@@ -51,10 +51,11 @@ enum class GemmKernel : int {
     Dma256 = 8,       // 256x256x16 tile, global -> LDS copies without VGPR staging
     Dma128 = 9,       // 128x128x32 tile, global -> LDS copies, two blocks per CU
     Dma64 = 10,       // 64x64x64 tile, global -> LDS copies, four waves of 32x32
+    Dma128W8 = 11,    // 128x128x64 tile, global -> LDS copies, eight waves of 64x32
     Auto = -1,
 };
 
-// Whether a direct-to-LDS kernel (Dma256, Dma128, Dma64) can run this problem:
+// Whether a direct-to-LDS kernel (Dma256, Dma128, Dma64, Dma128W8) can run this problem:
 // K a multiple of 4, both operands 16-byte vectorisable.
 bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
                    int64_t batch);

@@ -21,6 +21,7 @@ enum class GemmAlgo {
                     // 16-byte-aligned operands; std::runtime_error otherwise)
     MfmaDma128,     // 128x128x32 tile, same copies, two blocks per CU
     MfmaDma64,      // 64x64x64 tile, same copies, for mid-size problems
+    MfmaDma128W8,   // 128x128x64 tile, same copies, eight waves, one block per CU
 };
 
 const char* to_string(GemmAlgo algo);

@@ -73,7 +73,7 @@ def test_other_entry_points_validate():
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 1, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
                          1, None, None, 0, 3, None) == -2  # skinny with B transposed
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
-                         1, None, None, 0, 11, None) == -1
+                         1, None, None, 0, 12, None) == -1
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 22, 1 << 20, 24, 0, 1 << 20, 16, 0,
                          1 << 20, 16, 0, 1, None, None, 0, capi.KERNEL_DMA256, None) == -2
     assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
@@ -94,13 +94,15 @@ def test_kernel_choice():
     assert capi.kernel_choice(0, 0, 1000, 1000, 1000) == capi.KERNEL_DMA64
     assert capi.kernel_choice(0, 0, 1023, 1023, 1023) in (capi.KERNEL_SPLITK32,
                                                           capi.KERNEL_SPLITK16)
-    # too few 256x256 tiles to fill the GPU: the two-blocks-per-CU 128x128 tile
-    assert capi.kernel_choice(0, 0, 2048, 2048, 2048) == capi.KERNEL_DMA128
+    # about one 128x128 tile per CU: the eight-wave 128x128 tile; three per CU:
+    # the two-blocks-per-CU 128x128 tile
+    assert capi.kernel_choice(0, 0, 2048, 2048, 2048) == capi.KERNEL_DMA128W8
     assert capi.kernel_choice(0, 0, 4000, 3000, 2048) == capi.KERNEL_DMA128
     # K not a multiple of 4 rules the direct-to-LDS tiles out
     assert capi.kernel_choice(0, 0, 2048, 2048, 2050) not in (capi.KERNEL_DMA128,
                                                               capi.KERNEL_DMA256,
-                                                              capi.KERNEL_DMA64)
+                                                              capi.KERNEL_DMA64,
+                                                              capi.KERNEL_DMA128W8)
     assert capi.kernel_choice(0, 0, 8, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 8, 4096, 4096) != capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 0, 256, 128, 784) == capi.KERNEL_SPLITK16

@@ -1,5 +1,6 @@
 """GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256, K-tile 16;
-FDL_KERNEL_DMA128, K-tile 32; FDL_KERNEL_DMA64, K-tile 64) and of their
+FDL_KERNEL_DMA128, K-tile 32; FDL_KERNEL_DMA64 and FDL_KERNEL_DMA128W8, K-tile
+64) and of their
 dispatch rules: they run where K is a multiple of 4 (a partial last K-tile is
 clamped and masked) and both operands are 16-byte vectorisable, refuse other
 problems with FDL_ERROR_NOT_SUPPORTED when forced, and the automatic choice
@@ -14,7 +15,8 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, s
 pytestmark = pytest.mark.gpu
 
 DMA = capi.KERNEL_DMA256
-DMAS = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32), (capi.KERNEL_DMA64, 64)]
+DMAS = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32), (capi.KERNEL_DMA64, 64),
+        (capi.KERNEL_DMA128W8, 64)]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 # M and N multiples of 4 (either may be the contiguous extent), ragged against
 # the tiles; K in K-tiles (16 or 32 each) covering 1, 2, 3 and many K-tiles.
@@ -134,25 +136,27 @@ def test_dma_refuses_unsupported_problems(device):
     torch.cuda.synchronize()
 
 
-def test_auto_choice_and_misaligned_fallback(device):
+@pytest.mark.parametrize("M,N,K,fam", [(4096, 4096, 64, capi.KERNEL_DMA256),
+                                        (2048, 2048, 64, capi.KERNEL_DMA128W8)])
+def test_auto_choice_and_misaligned_fallback(device, M, N, K, fam):
     import torch
 
-    M, N, K = 4096, 4096, 64
-    assert capi.kernel_choice(0, 0, M, N, K) == DMA
-    g = _rng(17)
+    assert capi.kernel_choice(0, 0, M, N, K) == fam
+    g = _rng(17, M)
     A, B = operands(g, 0, 0, M, N, K, 1)
     # Operands placed one float past a 16-byte boundary: the automatic choice
-    # must fall back to the register-staged kernel and still be right.
+    # must fall back to the register-staged kernel with the same tile and
+    # still be right.
     dA = torch.zeros(M * K + 4, device="cuda")
     dB = torch.zeros(K * N + 4, device="cuda")
     dA[1:1 + M * K] = dev(A.reshape(-1))
     dB[1:1 + K * N] = dev(B.reshape(-1))
     dC = torch.full((M, N), float("nan"), device="cuda")
-    say("auto 4096x4096x64 misaligned operands")
+    say(f"auto {M}x{N}x{K} misaligned operands")
     capi.sgemm_ex(0, 0, M, N, K, dA.data_ptr() + 4, K, 0, dB.data_ptr() + 4, N, 0,
                   dC.data_ptr(), N, 0, 1, None, None, 0, stream())
     check_gemm(host(dC)[None], 0, 0, A, B, M, N, K)
-    say("auto 4096x4096x64 aligned operands (dma256)")
+    say(f"auto {M}x{N}x{K} aligned operands ({capi.KERNEL_NAMES[fam]})")
     dC.fill_(float("nan"))
     capi.sgemm_ex(0, 0, M, N, K, dA.data_ptr(), K, 0, dB.data_ptr(), N, 0,
                   dC.data_ptr(), N, 0, 1, None, None, 0, stream())
