@@ -42,6 +42,7 @@ PROFILE_CONFIGS = {
     "c5a_m8": (8, 4096, 4096, 0, 1, 2, 6),
     "c5b_777": (777, 777, 777, 0, 1, 2, 1),
     "c5b_1000": (1000, 1000, 1000, 0, 1, 2, 1),
+    "c5b_1023": (1023, 1023, 1023, 0, 1, 2, 1),
     "c2_mlp": "mlp",
 }
 
@@ -57,6 +58,10 @@ def parse_args():
     ap.add_argument("--sweep", default=None, help="write every BASELINE config's timing here")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the headline launches (for rocprofv3 runs)")
+    ap.add_argument("--profile-vendor", action="store_true",
+                    help="with --profile-mode: launch the same workload through PyTorch "
+                         "(vendor BLAS; eager autograd step for c2_mlp) instead, for "
+                         "comparison traces")
     ap.add_argument("--profile-config", default="headline", choices=sorted(PROFILE_CONFIGS),
                     help="with --profile-mode: which BASELINE configuration to launch")
     ap.add_argument("--copy-calib", action="store_true",
@@ -83,6 +88,8 @@ def warm_clock(fn, stream, ms=50.0, min_launch_ms=0.015):
     cost, which a long burst of launches beforehand was measured to raise."""
     import torch
 
+    fn()  # one-time costs (code load, first-touch) stay out of the estimate
+    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -387,17 +394,29 @@ def main():
     stream = torch.cuda.current_stream()
     if args.profile_mode and args.profile_config != "headline":
         cfg = PROFILE_CONFIGS[args.profile_config]
-        if cfg == "mlp":
+        if cfg == "mlp" and args.profile_vendor:
+            _, pms = torch_mlp_rate(torch, steps=args.steps, warmup=args.warmup)
+        elif cfg == "mlp":
             _, pms, _, _, _ = mlp_rate(capi, torch, steps=args.steps, warmup=args.warmup)
         else:
             M, N, K, tb, batch, epi, rot = cfg
-            plaunch, *_ = gemm_case(capi, torch, M, N, K, tb=tb, batch=batch, epi=epi,
-                                    rotate=rot)
+            if args.profile_vendor:
+                plaunch = vendor_case(torch, M, N, K, tb=tb, batch=batch, epi=epi, rotate=rot)
+            else:
+                plaunch, *_ = gemm_case(capi, torch, M, N, K, tb=tb, batch=batch, epi=epi,
+                                        rotate=rot)
+            # Timed on a warmed clock, as the sweep rows are.
+            warm_clock(plaunch, stream)
             pms = time_launches(plaunch, args.steps, args.warmup, stream)
         print(json.dumps({"profile_mode": True, "config": args.profile_config,
-                          "ms_per_launch": pms}), flush=True)
+                          "vendor": args.profile_vendor, "ms_per_launch": pms}), flush=True)
         return
     n = args.size
+    if args.profile_mode and args.profile_vendor:
+        vms = time_launches(vendor_case(torch, n, n, n), args.steps, args.warmup, stream)
+        print(json.dumps({"profile_mode": True, "config": "headline", "vendor": True,
+                          "ms_per_launch": vms}), flush=True)
+        return
     launch, A, B, C = gemm_case(capi, torch, n, n, n, seed=0)
     ms = time_launches(launch, args.steps, args.warmup, stream)
     if args.profile_mode:
