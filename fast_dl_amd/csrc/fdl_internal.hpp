@@ -50,7 +50,7 @@ enum class GemmKernel : int {
     SplitK16 = 7,     // 16x16 output tile (16x16x4 MFMA), K split over waves
     Dma256 = 8,       // 256x256x16 tile, global -> LDS copies without VGPR staging
     Dma128 = 9,       // 128x128x32 tile, global -> LDS copies, two blocks per CU
-    Dma64 = 10,       // 64x64x64 tile, global -> LDS copies, four waves of 32x32
+    Dma64 = 10,       // 64x64x64 tile, global -> LDS copies, two sets of four 32x32 waves
     Dma128W8 = 11,    // 128x128x64 tile, global -> LDS copies, eight waves of 64x32
     Auto = -1,
 };

@@ -445,13 +445,16 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // of 4).  Rows (columns) past M (N) are clamped to the last valid one: they
 // only feed accumulators that are never stored.
 // ---------------------------------------------------------------------------
+// KS > 1 splits each K-tile's k-groups over KS sets of waves that share the
+// block's LDS stages (more waves per SIMD for the same tile); their partial
+// sums are added in set order after the K loop.
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
-          int ILV_ = 0>
+          int ILV_ = 0, int KS_ = 1>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int STAGES = STAGES_;
-    static constexpr int XPIPE = XPIPE_, ILV = ILV_;
-    static constexpr int NT = kWave * (BM / WM) * (BN / WN);
+    static constexpr int XPIPE = XPIPE_, ILV = ILV_, KS = KS_;
+    static constexpr int NT = kWave * (BM / WM) * (BN / WN) * KS;
 };
 
 // s_waitcnt immediate: wait until at most n vector-memory operations of this
@@ -596,6 +599,11 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
     constexpr int NT = Cfg::NT, S = Cfg::STAGES;
     constexpr int FM = WM / 32, FN = WN / 32, WGM = BM / WM;
     constexpr int NG = BK / 8;
+    constexpr int KS = Cfg::KS;
+    constexpr int WMN = (BM / WM) * (BN / WN);  // waves of one k-group set
+    constexpr int NGK = NG / KS;                // k-groups per tile for each set
+    static_assert(NG % KS == 0, "the k-groups of a tile divide evenly over the sets");
+    static_assert(KS == 1 || Cfg::XPIPE != 0, "k-group sets need the cross-tile pipeline");
     using OpA = DmaOperand<BM, BK, NT, !TA>;
     using OpB = DmaOperand<BN, BK, NT, TB>;
     constexpr int PER_TILE = OpA::PER + OpB::PER;
@@ -609,8 +617,11 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
     const int wave = tid / kWave;
     const int l32 = lane & 31;
     const int half = lane >> 5;
-    const int wm0 = (wave % WGM) * WM;
-    const int wn0 = (wave / WGM) * WN;
+    const int kset = wave / WMN;                // which k-group set
+    const int wmn = wave % WMN;
+    const int wm0 = (wmn % WGM) * WM;
+    const int wn0 = (wmn / WGM) * WN;
+    const int g0 = kset * NGK;                  // this set's first k-group of a tile
 
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
@@ -724,7 +735,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         // those MFMAs run.  At the barrier every wave has read all of tile t
         // (lgkmcnt 0) and tile t+1 has landed (vmcnt 0: it is the only copy in
         // flight), so tile t+2 can go into tile t's stage right after it.
-        static_assert(S == 2 && NG % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
+        static_assert(S == 2 && NGK % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
         using No = std::false_type;
         using Yes = std::true_type;
         const bool has_tail = tail_tile >= 0;
@@ -738,9 +749,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (tail_tile == 0) {
-            read_group(As, Bs, 0, 0, 0, Yes{});
+            read_group(As, Bs, g0, 0, 0, Yes{});
         } else {
-            read_group(As, Bs, 0, 0, 0, No{});
+            read_group(As, Bs, g0, 0, 0, No{});
         }
         // One K-tile of the steady state (tiles t+1 and t+2 exist and are
         // wholly inside K).  Nothing here branches, so each group's fragment
@@ -751,9 +762,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             const float* as = As + cur * OpA::STAGE;
             const float* bs = Bs + cur * OpB::STAGE;
 #pragma unroll
-            for (int g = 0; g + 1 < NG; ++g) {
+            for (int g = 0; g + 1 < NGK; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                read_group(as, bs, g + 1, (g + 1) & 1, t, No{});
+                read_group(as, bs, g0 + g + 1, (g + 1) & 1, t, No{});
                 mfma_group(g & 1);
                 interleave_hint();
                 __builtin_amdgcn_sched_barrier(0);
@@ -768,8 +779,8 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             // last group's MFMAs.
             opa.issue_full(A, p.lda, (t + 2) * BK, As + cur * OpA::STAGE);
             opb.issue_full(B, p.ldb, (t + 2) * BK, Bs + cur * OpB::STAGE);
-            read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1, No{});
-            mfma_group((NG - 1) & 1);
+            read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, g0, 0, t + 1, No{});
+            mfma_group((NGK - 1) & 1);
             interleave_hint_copies();
             __builtin_amdgcn_sched_barrier(0);
         };
@@ -787,9 +798,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             const float* as = As + cur * OpA::STAGE;
             const float* bs = Bs + cur * OpB::STAGE;
 #pragma unroll
-            for (int g = 0; g + 1 < NG; ++g) {
+            for (int g = 0; g + 1 < NGK; ++g) {
                 __builtin_amdgcn_sched_barrier(0);
-                read_rt(as, bs, g + 1, (g + 1) & 1, t);
+                read_rt(as, bs, g0 + g + 1, (g + 1) & 1, t);
                 mfma_group(g & 1);
                 interleave_hint();
                 __builtin_amdgcn_sched_barrier(0);
@@ -801,9 +812,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
             if (t + 2 < ktiles) issue_tile(t + 2, cur);
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < ktiles) {
-                read_rt(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, 0, 0, t + 1);
+                read_rt(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, g0, 0, t + 1);
             }
-            mfma_group((NG - 1) & 1);
+            mfma_group((NGK - 1) & 1);
             interleave_hint();
             __builtin_amdgcn_sched_barrier(0);
         };
@@ -855,6 +866,37 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         }
     }
 
+    if constexpr (KS > 1) {
+        // The other sets' partial sums meet set 0's in LDS (the stages are
+        // free: every copy has landed and every wave is past its last read),
+        // added in set order.
+        constexpr int kPart = FM * FN * 16 * kWave;  // floats of one wave's accumulators
+        static_assert((KS - 1) * WMN * kPart <= S * (OpA::STAGE + OpB::STAGE),
+                      "partial sums fit in the LDS stages");
+        __syncthreads();
+        if (kset > 0) {
+            float* dst = lds + ((kset - 1) * WMN + wmn) * kPart + lane;
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[((mi * FN + ni) * 16 + r) * kWave] = acc[mi][ni][r];
+        }
+        __syncthreads();
+        if (kset > 0) return;
+#pragma unroll
+        for (int ks = 1; ks < KS; ++ks) {
+            const float* src = lds + ((ks - 1) * WMN + wmn) * kPart + lane;
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[mi][ni][r] += src[((mi * FN + ni) * 16 + r) * kWave];
+        }
+    }
     store_wave_tile<FM, FN>(acc, p, bz, m0 + wm0, n0 + wn0, half, l32);
 }
 
@@ -1531,9 +1573,11 @@ using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
 // 4000x3000x2048: 0.45 vs 0.54 ms for the 256x256 tile).
 using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
 using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
-// 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU
-// (1024^3: 29.7 us vs 42 us for the split-K kernel; 1000^3: 30 vs 43 us).
-using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1>;
+// 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU.  Two
+// sets of four 32x32 waves split each K-tile's k-groups, so one block per CU
+// still runs two waves per SIMD (1024^3: 24.3 vs 25.9 us with one set, and
+// 42 us for the split-K kernel).
+using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2>;
 // 128x128x64 with eight waves of 64x32 and 128 KB of LDS (one block per CU):
 // two waves per SIMD where the GPU holds about one 128x128 tile per CU
 // (2048^3: 131 vs 136.5 us for Dma128 in the same run).
@@ -1554,7 +1598,7 @@ struct TileModel {
 constexpr TileModel kTileModels[] = {
     {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f}},
     {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.75f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f}},
-    {GemmKernel::Dma64, 64, 64, 2, 4, {0, 0.535f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f, 0.705f}},
+    {GemmKernel::Dma64, 64, 64, 2, 8, {0, 0.57f, 0.57f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f}},
     {GemmKernel::Dma128W8, 128, 128, 1, 8, {0, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f}},
     {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},

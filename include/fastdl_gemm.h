@@ -101,7 +101,8 @@ typedef enum fdl_kernel {
                                   (base, ld and batch stride multiples of 4 floats,
                                   the contiguous extent a multiple of 4)          */
     FDL_KERNEL_DMA128 = 9,     /* 128x128x32 tile, two blocks per CU, same copies  */
-    FDL_KERNEL_DMA64 = 10,     /* 64x64x64 tile, four waves of 32x32, same copies  */
+    FDL_KERNEL_DMA64 = 10,     /* 64x64x64 tile, same copies; two sets of four
+                                  32x32 waves split each K-tile                    */
     FDL_KERNEL_DMA128W8 = 11   /* 128x128x64 tile, eight waves of 64x32, one block
                                   per CU, same copies                              */
 } fdl_kernel;
