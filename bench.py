@@ -454,6 +454,7 @@ def main():
     kernel = capi.KERNEL_NAMES.get(family, "auto")
     kernel_fn = {capi.KERNEL_DMA256: "sgemm_dma_kernel", capi.KERNEL_DMA128: "sgemm_dma_kernel",
                  capi.KERNEL_DMA64: "sgemm_dma_kernel", capi.KERNEL_DMA128W8: "sgemm_dma_kernel",
+                 capi.KERNEL_DMA64U: "sgemm_dma_kernel", capi.KERNEL_DMA128W8U: "sgemm_dma_kernel",
                  capi.KERNEL_SKINNY: "sgemm_skinny_kernel",
                  capi.KERNEL_SPLITK32: "sgemm_splitk32_kernel",
                  capi.KERNEL_SPLITK16: "sgemm_splitk16_kernel"}.get(family, "sgemm_tiled_kernel")

@@ -17,6 +17,8 @@ from .capi import (  # noqa: F401
     KERNEL_AUTO,
     KERNEL_DMA64,
     KERNEL_DMA128W8,
+    KERNEL_DMA128W8U,
+    KERNEL_DMA64U,
     KERNEL_DMA128,
     KERNEL_DMA256,
     KERNEL_SKINNY,

@@ -23,6 +23,8 @@ const char* to_string(GemmAlgo algo) {
         case GemmAlgo::MfmaDma128: return "mfma_dma128";
         case GemmAlgo::MfmaDma64: return "mfma_dma64";
         case GemmAlgo::MfmaDma128W8: return "mfma_dma128w8";
+        case GemmAlgo::MfmaDma64U: return "mfma_dma64u";
+        case GemmAlgo::MfmaDma128W8U: return "mfma_dma128w8u";
     }
     return "unknown";
 }
@@ -40,6 +42,8 @@ int kernel_id(GemmAlgo algo) {
         case GemmAlgo::MfmaDma128: return FDL_KERNEL_DMA128;
         case GemmAlgo::MfmaDma64: return FDL_KERNEL_DMA64;
         case GemmAlgo::MfmaDma128W8: return FDL_KERNEL_DMA128W8;
+        case GemmAlgo::MfmaDma64U: return FDL_KERNEL_DMA64U;
+        case GemmAlgo::MfmaDma128W8U: return FDL_KERNEL_DMA128W8U;
     }
     return FDL_KERNEL_AUTO;
 }

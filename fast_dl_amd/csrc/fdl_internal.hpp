@@ -52,11 +52,15 @@ enum class GemmKernel : int {
     Dma128 = 9,       // 128x128x32 tile, global -> LDS copies, two blocks per CU
     Dma64 = 10,       // 64x64x64 tile, global -> LDS copies, two sets of four 32x32 waves
     Dma128W8 = 11,    // 128x128x64 tile, global -> LDS copies, eight waves of 64x32
+    Dma64U = 12,      // Dma64 with 4-byte copies (any K, leading dimension, alignment)
+    Dma128W8U = 13,   // Dma128W8 with 4-byte copies
     Auto = -1,
 };
 
-// Whether a direct-to-LDS kernel (Dma256, Dma128, Dma64, Dma128W8) can run this problem:
-// K a multiple of 4, both operands 16-byte vectorisable.
+// Whether a direct-to-LDS kernel can run this problem.  The 16-byte-copy
+// ones (Dma256, Dma128, Dma64, Dma128W8) need K a multiple of 4 and both
+// operands 16-byte vectorisable; the 4-byte-copy ones (Dma64U, Dma128W8U)
+// need leading dimensions up to 2^24 and 4-byte-aligned pointers.
 bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
                    int64_t batch);
 

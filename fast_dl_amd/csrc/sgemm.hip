@@ -448,12 +448,14 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // KS > 1 splits each K-tile's k-groups over KS sets of waves that share the
 // block's LDS stages (more waves per SIMD for the same tile); their partial
 // sums are added in set order after the K loop.
+// CW is the copy width in floats per lane (4: 16-byte copies, which need
+// 16-byte-aligned operand rows and K % 4 == 0; 1: 4-byte copies, any shape).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
-          int ILV_ = 0, int KS_ = 1>
+          int ILV_ = 0, int KS_ = 1, int CW_ = 4>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int STAGES = STAGES_;
-    static constexpr int XPIPE = XPIPE_, ILV = ILV_, KS = KS_;
+    static constexpr int XPIPE = XPIPE_, ILV = ILV_, KS = KS_, CW = CW_;
     static constexpr int NT = kWave * (BM / WM) * (BN / WN) * KS;
 };
 
@@ -466,6 +468,26 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) |
 // host pass, which cannot type-check this device builtin, never sees it.
 __device__ __forceinline__ void dma_copy16(const float* g, float* lds) {
     __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// The same with 4 bytes per lane (lane i writes lds + i floats).
+__device__ __forceinline__ void dma_copy4(const float* g, float* lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
+}
+
+// 4-byte copies through a buffer descriptor: `base` is wave-uniform (scalar
+// registers) and each lane adds its own 32-bit byte offset, so a copy costs
+// one VGPR instead of a 64-bit address.  Descriptor word 3 is the raw-buffer
+// value for gfx9-family targets (gfx950 included).
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_buffer(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, kBufferWord3);
+}
+
+__device__ __forceinline__ void dma_buf_copy4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off,
+                                              float* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 4, byte_off, 0, 0, 0);
 }
 
 // Chunk permutation of a k-contiguous LDS row of CPR 16-byte chunks.  Both
@@ -481,49 +503,92 @@ __device__ __forceinline__ int kc_swz(int r) {
     return r & 15;  // 16 chunks: measured conflict-free, (r >> 1) & 15 costs 10%
 }
 
-template <int MN, int BK, int NT, bool KC>
+// One global -> LDS copy operand.  CW is the copy width in floats per lane:
+// 4 (16-byte copies; needs 16-byte-aligned rows) or 1 (4-byte copies; any
+// alignment, any K).  Either way the LDS image is the same, so the fragment
+// reads are shared: a k-contiguous operand is stored as rows of BK floats
+// whose 16-byte chunks are rotated by kc_swz, an mn-contiguous operand as
+// unpadded rows of MN floats.  With CW = 1 a copy's 64 lanes fill 64
+// consecutive LDS floats, each lane fetching the global element that belongs
+// there, so one copy still reads one contiguous row segment.
+template <int MN, int BK, int NT, bool KC, int CW = 4>
 struct DmaOperand {
     static constexpr int CPR = BK / 4;                     // k chunks per k-contiguous row
     static constexpr int LDR = KC ? BK : MN;               // floats per LDS row
     static constexpr int STAGE = MN * BK;                  // floats per stage
-    static constexpr int CHUNKS = MN * BK / 4;
-    static constexpr int PER = CHUNKS / NT;                // copies per lane per tile
-    static constexpr int ROW_CHUNKS = MN / 4;              // chunks per mn-contiguous row
-    static_assert(CHUNKS % NT == 0, "copies must divide evenly");
+    static constexpr int UNITS = MN * BK / CW;             // copy units per stage
+    static constexpr int PER = UNITS / NT;                 // copies per lane per tile
+    static_assert(CW == 4 || CW == 1, "16- or 4-byte copies");
+    static_assert(UNITS % NT == 0, "copies must divide evenly");
     static_assert(!KC || CPR == 4 || CPR == 8 || CPR == 16,
                   "BK of 16, 32 or 64 for a k-contiguous operand");
-    static_assert(KC || (kWave % ROW_CHUNKS == 0 || ROW_CHUNKS % kWave == 0),
+    static_assert(!KC || (kWave * CW) % BK == 0, "a copy covers whole k-contiguous rows");
+    static_assert(CW == 4 || !KC || BK == kWave, "4-byte copies of k-contiguous rows: BK = 64");
+    static_assert(KC || (kWave * CW) % MN == 0 || MN % (kWave * CW) == 0,
                   "mn-contiguous rows must tile the 64-lane copies");
-    int64_t goff[PER];  // this lane's global offset of each copy at k0 = 0
+    // Global offset of each copy at k0 = 0.  With CW = 4 it is a 64-bit
+    // value per lane (goff).  With CW = 1 it is the wave's base (gb0, the row
+    // of its first copy; wave-uniform, so in scalar registers) plus a 32-bit
+    // lane part per copy (lo): the 2-4x more copies cost one VGPR each.  The
+    // lane part spans at most PER rows: callers keep ld * PER below 2^31.
+    static constexpr int P4 = CW == 4 ? PER : 1;
+    static constexpr int P1 = CW == 1 ? PER : 1;
+    int64_t goff[P4];
+    int64_t gb0;
+    int lo[P1];
     int loff[PER];      // wave-uniform LDS offset (floats) of each copy within a stage
+
+    // Position (in the tile) of copy unit `slot`: the operand row or k row
+    // `r`, and the offset along the contiguous dimension `c`.
+    __device__ __forceinline__ static void place(int slot, int& r, int& c) {
+        const int f = slot * CW;  // LDS float offset within the stage
+        if (KC) {
+            r = f / BK;
+            const int p = f % BK;
+            c = 4 * ((p / 4) ^ kc_swz<CPR>(r)) + p % 4;  // global k within the tile
+        } else {
+            r = f / MN;  // k row
+            c = f % MN;  // column
+        }
+    }
 
     __device__ __forceinline__ void init(int64_t ld, int mn0, int mn_lim, int tid) {
         const int lane = tid & (kWave - 1);
         // Wave-uniform by construction; readfirstlane lets the compiler keep
         // loff in scalar registers, so each copy sets M0 without a VALU step.
         const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+        // Row of the wave's first copy (the same for every lane).
+        int r0, c0;
+        place(wave * PER * kWave, r0, c0);
+        const int row0 = KC ? min(mn0 + r0, mn_lim - 1) : r0;
+        gb0 = (int64_t)row0 * ld;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int ins = wave * PER + i;
-            const int slot = ins * kWave + lane;
-            if (KC) {
-                const int r = slot / CPR;
-                const int c = (slot % CPR) ^ kc_swz<CPR>(r);
-                goff[i] = (int64_t)min(mn0 + r, mn_lim - 1) * ld + 4 * c;
+            int r, c;
+            place(ins * kWave + lane, r, c);
+            if constexpr (CW == 4) {
+                if (KC) {
+                    goff[i] = (int64_t)min(mn0 + r, mn_lim - 1) * ld + c;
+                } else {
+                    goff[i] = (int64_t)r * ld + min(mn0 + c, mn_lim - 4);
+                }
             } else {
-                const int k = slot / ROW_CHUNKS;
-                const int col = (slot % ROW_CHUNKS) * 4;
-                goff[i] = (int64_t)k * ld + min(mn0 + col, mn_lim - 4);
+                if (KC) {
+                    lo[i] = (int)((int64_t)(min(mn0 + r, mn_lim - 1) - row0) * ld) + c;
+                } else {
+                    lo[i] = (int)((int64_t)(r - row0) * ld) + min(mn0 + c, mn_lim - 1);
+                }
             }
-            loff[i] = ins * kWave * 4;
+            loff[i] = ins * kWave * CW;
         }
     }
 
     // Copies the tile whose first reduction index is k0 into `stage`.  In
-    // the tile that crosses K (K a multiple of 4, so a chunk is either wholly
-    // inside or wholly past K) the copies past K are redirected to the last
-    // valid chunk or row: the kernel zeroes the fragment values read from
-    // those slots, so they never count.
+    // the tile that crosses K the copies past K are redirected to the last
+    // valid element or row (with CW = 4, K is a multiple of 4, so a chunk is
+    // either wholly inside or wholly past K): the kernel zeroes the fragment
+    // values read from those slots, so they never count.
     __device__ __forceinline__ void issue(const float* __restrict__ base, int64_t ld, int k0,
                                           int K, float* stage, int tid) const {
         if (k0 + BK <= K) {
@@ -533,12 +598,28 @@ struct DmaOperand {
         }
     }
 
+    __device__ __forceinline__ static void copy(const float* g, float* lds) {
+        if (CW == 4) {
+            dma_copy16(g, lds);
+        } else {
+            dma_copy4(g, lds);
+        }
+    }
+
     // A tile wholly inside K: no per-copy bounds work.
     __device__ __forceinline__ void issue_full(const float* __restrict__ base, int64_t ld, int k0,
                                                float* stage) const {
         const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
+        if constexpr (CW == 4) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) dma_copy16(base + goff[i] + koff, stage + loff[i]);
+            for (int i = 0; i < PER; ++i) copy(base + goff[i] + koff, stage + loff[i]);
+        } else {
+            // The tile's wave-uniform base in a buffer descriptor (scalar
+            // registers), each copy's lane part as a 32-bit offset from it.
+            const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
+#pragma unroll
+            for (int i = 0; i < PER; ++i) dma_buf_copy4(rsrc, (uint32_t)lo[i] * 4u, stage + loff[i]);
+        }
     }
 
     __device__ __forceinline__ void issue_tail(const float* __restrict__ base, int64_t ld, int k0,
@@ -547,16 +628,16 @@ struct DmaOperand {
         const int wave = tid / kWave;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int slot = (wave * PER + i) * kWave + lane;
+            int r, c;
+            place((wave * PER + i) * kWave + lane, r, c);
+            const int64_t g = CW == 4 ? goff[i] : gb0 + lo[i];
             int64_t off;
             if (KC) {
-                const int kc = 4 * ((slot % CPR) ^ kc_swz<CPR>(slot / CPR));
-                off = goff[i] - kc + min(k0 + kc, K - 4);
+                off = g - c + min(k0 + c, K - CW);
             } else {
-                const int kr = slot / ROW_CHUNKS;
-                off = goff[i] + (int64_t)(min(k0 + kr, K - 1) - kr) * ld;
+                off = g + (int64_t)(min(k0 + r, K - 1) - r) * ld;
             }
-            dma_copy16(base + off, stage + loff[i]);
+            copy(base + off, stage + loff[i]);
         }
     }
 
@@ -604,10 +685,11 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
     constexpr int NGK = NG / KS;                // k-groups per tile for each set
     static_assert(NG % KS == 0, "the k-groups of a tile divide evenly over the sets");
     static_assert(KS == 1 || Cfg::XPIPE != 0, "k-group sets need the cross-tile pipeline");
-    using OpA = DmaOperand<BM, BK, NT, !TA>;
-    using OpB = DmaOperand<BN, BK, NT, TB>;
+    using OpA = DmaOperand<BM, BK, NT, !TA, Cfg::CW>;
+    using OpB = DmaOperand<BN, BK, NT, TB, Cfg::CW>;
     constexpr int PER_TILE = OpA::PER + OpB::PER;
     static_assert(S >= 2 && S <= 4, "2 to 4 stages");
+    static_assert((S - 1) * PER_TILE <= 63, "copies in flight fit the 6-bit vmcnt counter");
     __shared__ __attribute__((aligned(16))) float lds[S * (OpA::STAGE + OpB::STAGE)];
     float* const As = lds;
     float* const Bs = lds + S * OpA::STAGE;
@@ -1582,6 +1664,11 @@ using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2>;
 // two waves per SIMD where the GPU holds about one 128x128 tile per CU
 // (2048^3: 131 vs 136.5 us for Dma128 in the same run).
 using CfgDma128W8 = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1>;
+// The same tiles with 4-byte copies: any K, any leading dimension, any
+// 4-byte-aligned pointer, at 2-3% below their 16-byte twins (1023^3: 26.5 us
+// against 44 us for split-K; 4095^3: 1.11 ms).
+using CfgDma64U = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2, 1>;
+using CfgDma128W8U = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1, 1, 1>;
 
 // Dispatch cost model.  A config runs `slots` blocks per CU at full
 // occupancy (LDS and register bound), each block holding `waves` waves; eff[w]
@@ -1600,6 +1687,8 @@ constexpr TileModel kTileModels[] = {
     {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.75f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f}},
     {GemmKernel::Dma64, 64, 64, 2, 8, {0, 0.57f, 0.57f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f}},
     {GemmKernel::Dma128W8, 128, 128, 1, 8, {0, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f}},
+    {GemmKernel::Dma64U, 64, 64, 2, 8, {0, 0.553f, 0.553f, 0.67f, 0.67f, 0.67f, 0.67f, 0.67f, 0.67f}},
+    {GemmKernel::Dma128W8U, 128, 128, 1, 8, {0, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f}},
     {GemmKernel::Tiled256, 256, 256, 1, 8, {0, 0.50f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled256x128, 256, 128, 2, 8, {0, 0.45f, 0.70f, 0.74f, 0.79f, 0.79f, 0.79f, 0.79f, 0.79f}},
     {GemmKernel::Tiled128, 128, 128, 3, 4, {0, 0.565f, 0.66f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f, 0.71f}},
@@ -1623,26 +1712,40 @@ double predicted_time(const TileModel& t, int M, int N, int64_t batch) {
     return time;
 }
 
+// Direct-to-LDS kernels with 4-byte copies (any shape).
+bool is_dma4(GemmKernel k) {
+    return k == GemmKernel::Dma64U || k == GemmKernel::Dma128W8U;
+}
+
 bool is_dma(GemmKernel k) {
     return k == GemmKernel::Dma256 || k == GemmKernel::Dma128 || k == GemmKernel::Dma64 ||
-           k == GemmKernel::Dma128W8;
+           k == GemmKernel::Dma128W8 || is_dma4(k);
 }
+
+// Largest leading dimension of the 4-byte-copy kernels: a copy's 32-bit
+// lane offset spans up to 32 rows of 4-byte elements.
+constexpr int64_t kDma4MaxLd = int64_t(1) << 24;
 
 // Shape part of a direct-to-LDS kernel's contract (pointers not needed).
 bool dma_shape_ok(GemmKernel k, const GemmParams& p, bool transA, bool transB) {
-    (void)k;
+    if (is_dma4(k)) return p.K >= 1 && p.lda <= kDma4MaxLd && p.ldb <= kDma4MaxLd;
     const int64_t a_contig = transA ? p.M : p.K;
     const int64_t b_contig = transB ? p.K : p.N;
     return p.K >= 4 && p.K % 4 == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
            p.lda % 4 == 0 && p.ldb % 4 == 0;
 }
 
+inline bool aligned4(const void* ptr) {
+    return (reinterpret_cast<uintptr_t>(ptr) & 3u) == 0;
+}
+
 }  // namespace
 
 bool dma_supported(GemmKernel k, const GemmParams& p, bool transA, bool transB,
                    int64_t batch) {
-    return is_dma(k) && dma_shape_ok(k, p, transA, transB) &&
-           vec_ok(p.A, transA ? p.M : p.K, p.lda, p.strideA, batch) &&
+    if (!is_dma(k) || !dma_shape_ok(k, p, transA, transB)) return false;
+    if (is_dma4(k)) return aligned4(p.A) && aligned4(p.B);
+    return vec_ok(p.A, transA ? p.M : p.K, p.lda, p.strideA, batch) &&
            vec_ok(p.B, transB ? p.K : p.N, p.ldb, p.strideB, batch);
 }
 
@@ -1660,6 +1763,8 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::Dma128: return "dma128";
         case GemmKernel::Dma64: return "dma64";
         case GemmKernel::Dma128W8: return "dma128w8";
+        case GemmKernel::Dma64U: return "dma64u";
+        case GemmKernel::Dma128W8U: return "dma128w8u";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -1674,30 +1779,34 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     constexpr int64_t kCUs = 256;
     // Too few 64x64 tiles to occupy the GPU, or too short a K loop to
     // amortise LDS staging: split K over the waves of a block instead, with
-    // 16x16 output tiles when 32x32 ones would leave most CUs idle.
-    // Below ~128 tiles of 128x128 the register-staged tile kernels cannot fill
-    // the GPU and the split-K kernels measure faster (the C4 batch of 64
-    // 128x128x64 problems: 5.8 vs 6.8 us); the 64x64 direct-to-LDS tile beats
-    // them once K is long enough (1024^3: 29.7 vs 42 us).
+    // 16x16 output tiles when 32x32 ones would leave most CUs idle.  Short K
+    // needs a full GPU of 64x64 tiles and ~128 tiles of 128x128 (the C4 batch
+    // of 64 128x128x64 problems: split-K 5.8 vs 6.8 us for a tile kernel);
+    // with K >= 256 the 64x64 direct-to-LDS tile wins from ~160 tiles
+    // (777^3: 21.9 vs 25.2 us; 1024^3: 22 vs 42 us).
     const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    const bool dma_mid = p.K >= 256 && dma_shape_ok(GemmKernel::Dma64, p, transA, transB);
-    if (t64 < kCUs || p.K < 64 || (t128 < 128 && !dma_mid)) {
+    const bool long_k = p.K >= 256;
+    if (p.K < 64 || t64 < (long_k ? 160 : kCUs) || (t128 < 128 && !long_k)) {
         const int64_t t32 = (int64_t)((p.M + 31) / 32) * ((p.N + 31) / 32) * batch;
         return t32 < 128 ? GemmKernel::SplitK16 : GemmKernel::SplitK32;
     }
+    // The direct-to-LDS tiles compete where their shape contract holds (the
+    // 4-byte-copy ones almost always); the register-staged tiles only when
+    // none does.  launch_sgemm moves a 16-byte choice to its 4-byte twin
+    // when the pointers turn out misaligned.
     GemmKernel best = GemmKernel::Tiled64;
     double best_time = 0.0;
     bool first = true;
-    for (const TileModel& t : kTileModels) {
-        // The direct-to-LDS kernels compete only where their shape contract
-        // holds; launch_sgemm falls back to the register-staged kernel with
-        // the same tile when the pointers are not 16-byte aligned.
-        if (is_dma(t.kernel) && !dma_shape_ok(t.kernel, p, transA, transB)) continue;
-        const double tm = predicted_time(t, p.M, p.N, batch);
-        if (first || tm < best_time * 0.99) {  // ties keep the earlier (larger) tile
-            best = t.kernel;
-            best_time = tm;
-            first = false;
+    for (int pass = 0; pass < 2 && first; ++pass) {
+        for (const TileModel& t : kTileModels) {
+            if (is_dma(t.kernel) != (pass == 0)) continue;
+            if (is_dma(t.kernel) && !dma_shape_ok(t.kernel, p, transA, transB)) continue;
+            const double tm = predicted_time(t, p.M, p.N, batch);
+            if (first || tm < best_time * 0.99) {  // ties keep the earlier (larger) tile
+                best = t.kernel;
+                best_time = tm;
+                first = false;
+            }
         }
     }
     return best;
@@ -1785,10 +1894,17 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
     if (kernel == GemmKernel::Skinny && (transB || p0.M > 8)) return hipErrorInvalidValue;
     if (is_dma(kernel) && !dma_supported(kernel, p0, transA, transB, batch)) {
         if (!automatic) return hipErrorInvalidValue;
-        kernel = kernel == GemmKernel::Dma256     ? GemmKernel::Tiled256
-                 : kernel == GemmKernel::Dma128   ? GemmKernel::Tiled128
-                 : kernel == GemmKernel::Dma128W8 ? GemmKernel::Tiled128W8
-                                                  : GemmKernel::Tiled64;
+        // Misaligned pointers: the 4-byte-copy tile, else the register-staged one.
+        const GemmKernel u = kernel == GemmKernel::Dma64 ? GemmKernel::Dma64U : GemmKernel::Dma128W8U;
+        if (!is_dma4(kernel) && dma_supported(u, p0, transA, transB, batch)) {
+            kernel = u;
+        } else {
+            kernel = kernel == GemmKernel::Dma256     ? GemmKernel::Tiled256
+                     : kernel == GemmKernel::Dma128   ? GemmKernel::Tiled128
+                     : kernel == GemmKernel::Dma128W8 ? GemmKernel::Tiled128W8
+                     : kernel == GemmKernel::Dma128W8U ? GemmKernel::Tiled128W8
+                                                      : GemmKernel::Tiled64;
+        }
     }
 
     const bool va = vec_ok(p0.A, transA ? p0.M : p0.K, p0.lda, p0.strideA, batch);
@@ -1838,6 +1954,12 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::Dma128W8:
                 err = launch_dma<CfgDma128W8>(p, transA, transB, nb, stream);
+                break;
+            case GemmKernel::Dma64U:
+                err = launch_dma<CfgDma64U>(p, transA, transB, nb, stream);
+                break;
+            case GemmKernel::Dma128W8U:
+                err = launch_dma<CfgDma128W8U>(p, transA, transB, nb, stream);
                 break;
             default:
                 return hipErrorInvalidValue;

@@ -22,6 +22,8 @@ enum class GemmAlgo {
     MfmaDma128,     // 128x128x32 tile, same copies, two blocks per CU
     MfmaDma64,      // 64x64x64 tile, same copies, for mid-size problems
     MfmaDma128W8,   // 128x128x64 tile, same copies, eight waves, one block per CU
+    MfmaDma64U,     // MfmaDma64 with 4-byte copies: any k, leading dimension, alignment
+    MfmaDma128W8U,  // MfmaDma128W8 with 4-byte copies
 };
 
 const char* to_string(GemmAlgo algo);

@@ -103,8 +103,12 @@ typedef enum fdl_kernel {
     FDL_KERNEL_DMA128 = 9,     /* 128x128x32 tile, two blocks per CU, same copies  */
     FDL_KERNEL_DMA64 = 10,     /* 64x64x64 tile, same copies; two sets of four
                                   32x32 waves split each K-tile                    */
-    FDL_KERNEL_DMA128W8 = 11   /* 128x128x64 tile, eight waves of 64x32, one block
+    FDL_KERNEL_DMA128W8 = 11,  /* 128x128x64 tile, eight waves of 64x32, one block
                                   per CU, same copies                              */
+    FDL_KERNEL_DMA64U = 12,    /* FDL_KERNEL_DMA64 with 4-byte copies: any K, any
+                                  leading dimension up to 2^24, any 4-byte-aligned
+                                  operand (odd shapes, unaligned views)            */
+    FDL_KERNEL_DMA128W8U = 13  /* FDL_KERNEL_DMA128W8 with 4-byte copies          */
 } fdl_kernel;
 
 /*

@@ -138,7 +138,8 @@ int main() {
         auto ta = dl::Tensor::from_host<float>(a, dl::Shape({m, k}), kDev);
         auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
         for (auto algo : {dl::kernels::GemmAlgo::MfmaDma256, dl::kernels::GemmAlgo::MfmaDma128,
-                          dl::kernels::GemmAlgo::MfmaDma64, dl::kernels::GemmAlgo::MfmaDma128W8}) {
+                          dl::kernels::GemmAlgo::MfmaDma64, dl::kernels::GemmAlgo::MfmaDma128W8,
+                          dl::kernels::GemmAlgo::MfmaDma64U, dl::kernels::GemmAlgo::MfmaDma128W8U}) {
             dl::Tensor tc(dl::Shape({m, n}), dl::DType::Float32, kDev);
             dl::kernels::gemm(static_cast<const float*>(ta.data()),
                               static_cast<const float*>(tb.data()), static_cast<float*>(tc.data()),
@@ -158,6 +159,19 @@ int main() {
                               static_cast<const float*>(b2.data()), static_cast<float*>(c2.data()),
                               m, n, k2, dl::kernels::GemmAlgo::MfmaDma128);
         } catch (const std::runtime_error&) {
+            // ... while the 4-byte-copy twins take it.
+            const auto want2 = host_gemm(a2.to_host<float>(), b2.to_host<float>(), m, n, k2);
+            for (auto algo : {dl::kernels::GemmAlgo::MfmaDma64U,
+                              dl::kernels::GemmAlgo::MfmaDma128W8U}) {
+                dl::kernels::gemm(static_cast<const float*>(a2.data()),
+                                  static_cast<const float*>(b2.data()),
+                                  static_cast<float*>(c2.data()), m, n, k2, algo);
+                if (!close(c2.to_host<float>(), want2, 1e-5f)) {
+                    std::cout << "  algo " << dl::kernels::to_string(algo) << " mismatch (k=50)"
+                              << std::endl;
+                    return false;
+                }
+            }
             return true;
         }
         std::cout << "  k % 4 != 0 was not refused" << std::endl;

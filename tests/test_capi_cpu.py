@@ -73,7 +73,7 @@ def test_other_entry_points_validate():
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 1, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
                          1, None, None, 0, 3, None) == -2  # skinny with B transposed
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
-                         1, None, None, 0, 12, None) == -1
+                         1, None, None, 0, 14, None) == -1
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 22, 1 << 20, 24, 0, 1 << 20, 16, 0,
                          1 << 20, 16, 0, 1, None, None, 0, capi.KERNEL_DMA256, None) == -2
     assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
@@ -84,16 +84,18 @@ def test_kernel_choice():
     assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_DMA256
     assert capi.kernel_choice(1, 1, 4096, 4096, 4096) == capi.KERNEL_DMA256
     # K not a multiple of 4, or B's contiguous extent not a multiple of 4:
-    # the register-staged kernel with the same tile
-    assert capi.kernel_choice(0, 0, 4096, 4096, 4098) == capi.KERNEL_TILED256
-    assert capi.kernel_choice(0, 0, 4096, 4094, 4096) == capi.KERNEL_TILED256
+    # the 4-byte-copy direct-to-LDS tiles
+    assert capi.kernel_choice(0, 0, 4096, 4096, 4098) == capi.KERNEL_DMA128W8U
+    assert capi.kernel_choice(0, 0, 4096, 4094, 4096) == capi.KERNEL_DMA128W8U
     # a partial last K-tile is fine for the direct-to-LDS kernels
     assert capi.kernel_choice(0, 0, 4096, 4096, 4100) == capi.KERNEL_DMA256
     # mid-size cubes: the 64x64 direct-to-LDS tile where K % 4 == 0
     assert capi.kernel_choice(0, 0, 1024, 1024, 1024) == capi.KERNEL_DMA64
     assert capi.kernel_choice(0, 0, 1000, 1000, 1000) == capi.KERNEL_DMA64
-    assert capi.kernel_choice(0, 0, 1023, 1023, 1023) in (capi.KERNEL_SPLITK32,
-                                                          capi.KERNEL_SPLITK16)
+    assert capi.kernel_choice(0, 0, 1023, 1023, 1023) == capi.KERNEL_DMA64U
+    assert capi.kernel_choice(0, 0, 777, 777, 777) == capi.KERNEL_DMA64U
+    # a short K stays on split-K (the C4 batch)
+    assert capi.kernel_choice(0, 0, 128, 128, 64, 64) == capi.KERNEL_SPLITK32
     # about one 128x128 tile per CU: the eight-wave 128x128 tile; three per CU:
     # the two-blocks-per-CU 128x128 tile
     assert capi.kernel_choice(0, 0, 2048, 2048, 2048) == capi.KERNEL_DMA128W8
