@@ -204,11 +204,72 @@ struct TileLoader {
 
 // Epilogue of the LDS-tiled kernels: one wave's FM x FN block of 32x32
 // accumulators, whose top-left element is C[mw][nw], goes through the
-// epilogue into C (bounds-checked per element).
+// epilogue into C.
+//
+// Interior wave blocks with an epilogue that reads nothing per element (none,
+// bias, bias+ReLU, ReLU) take a fast path: stores through a buffer descriptor
+// based at the block's corner, each lane's column and half-row as a 32-bit
+// offset and the row part wave-uniform (a scalar offset), so a store costs no
+// address arithmetic, no bounds test and no wait.  `bias_pre`, when given,
+// holds this lane's bias value of each column block, fetched before the K
+// loop.  The per-element path below it serves edge blocks and the epilogues
+// that read aux or update a parameter.
+constexpr int kBufferWord3Store = 0x00020000;  // raw-buffer descriptor word 3 (gfx9 family)
+
 template <int FM, int FN>
 __device__ __forceinline__ void store_wave_tile(floatx16 (&acc)[FM][FN], const GemmParams& p,
                                                 int64_t bz, int mw, int nw, int half,
-                                                int l32) {
+                                                int l32, const float* bias_pre = nullptr) {
+    {
+        const int epi = p.epilogue;
+        const bool plain = epi == EPI_NONE || epi == EPI_BIAS || epi == EPI_BIAS_RELU ||
+                           epi == EPI_RELU;
+        // Byte offsets stay below 2^31: (FM * 32 rows) * ldc * 4 bytes.
+        if (plain && mw + FM * 32 <= p.M && nw + FN * 32 <= p.N &&
+            p.ldc < (int64_t(1) << 29) / (FM * 32)) {
+            const bool has_bias = epi == EPI_BIAS || epi == EPI_BIAS_RELU;
+            const bool relu = epi == EPI_BIAS_RELU || epi == EPI_RELU;
+            // mw and nw are wave-uniform by construction; saying so keeps the
+            // descriptor in scalar registers.
+            const int mwu = __builtin_amdgcn_readfirstlane(mw);
+            const int nwu = __builtin_amdgcn_readfirstlane(nw);
+            float* corner = p.C + bz * p.strideC + (int64_t)mwu * p.ldc + nwu;
+            const __amdgpu_buffer_rsrc_t rsrc =
+                __builtin_amdgcn_make_buffer_rsrc(corner, (short)0, -1, kBufferWord3Store);
+            const int ldc = (int)p.ldc;
+            const uint32_t lane_off = (uint32_t)((4 * half) * ldc + l32) * 4u;
+            float bj[FN];
+#pragma unroll
+            for (int ni = 0; ni < FN; ++ni) {
+                bj[ni] = has_bias ? (bias_pre ? bias_pre[ni] : p.bias[nw + ni * 32 + l32]) : 0.0f;
+            }
+            // One uniform branch on the epilogue, then straight-line stores.
+            auto store_all = [&](auto op) __attribute__((always_inline)) {
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+                    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int row = mi * 32 + 8 * (r >> 2) + (r & 3);
+                            const float v = op(acc[mi][ni][r], bj[ni]);
+                            __builtin_amdgcn_raw_buffer_store_b32(
+                                __builtin_bit_cast(uint32_t, v), rsrc, (int)lane_off,
+                                (row * ldc + ni * 32) * 4, 0);
+                        }
+            };
+            if (has_bias && relu) {
+                store_all([](float v, float b) { return fmaxf(0.0f, v + b); });
+            } else if (has_bias) {
+                store_all([](float v, float b) { return v + b; });
+            } else if (relu) {
+                store_all([](float v, float) { return fmaxf(0.0f, v); });
+            } else {
+                store_all([](float v, float) { return v; });
+            }
+            return;
+        }
+    }
     float* __restrict__ C = p.C + bz * p.strideC;
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
     float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
@@ -451,11 +512,12 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // CW is the copy width in floats per lane (4: 16-byte copies, which need
 // 16-byte-aligned operand rows and K % 4 == 0; 1: 4-byte copies, any shape).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
-          int ILV_ = 0, int KS_ = 1, int CW_ = 4>
+          int ILV_ = 0, int KS_ = 1, int CW_ = 4, int WPE_ = 1>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int STAGES = STAGES_;
     static constexpr int XPIPE = XPIPE_, ILV = ILV_, KS = KS_, CW = CW_;
+    static constexpr int WPE = WPE_;  // waves per SIMD the register budget must allow
     static constexpr int NT = kWave * (BM / WM) * (BN / WN) * KS;
 };
 
@@ -674,7 +736,7 @@ __device__ __forceinline__ void spread_hint(std::integer_sequence<int, J...>) {
 }
 
 template <class Cfg, bool TA, bool TB>
-__global__ void __launch_bounds__(Cfg::NT)
+__global__ void __launch_bounds__(Cfg::NT, Cfg::WPE)
 sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, WM = Cfg::WM, WN = Cfg::WN;
     constexpr int NT = Cfg::NT, S = Cfg::STAGES;
@@ -725,6 +787,18 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
         for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+
+    // This lane's bias value of each column block, for the epilogue.  Issued
+    // before the first copies, so the explicit vmcnt counts of the copies below
+    // (which count only later operations) stay exact.
+    float bias_pre[FN];
+    if (p.epilogue == EPI_BIAS || p.epilogue == EPI_BIAS_RELU) {
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni) bias_pre[ni] = p.bias[min(n0 + wn0 + ni * 32 + l32, p.N - 1)];
+    } else {
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni) bias_pre[ni] = 0.0f;
+    }
 
     // K need only be a multiple of 4: the last K-tile may be partial.
     const int ktiles = (p.K + BK - 1) / BK;
@@ -979,7 +1053,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
                         acc[mi][ni][r] += src[((mi * FN + ni) * 16 + r) * kWave];
         }
     }
-    store_wave_tile<FM, FN>(acc, p, bz, m0 + wm0, n0 + wn0, half, l32);
+    store_wave_tile<FM, FN>(acc, p, bz, m0 + wm0, n0 + wn0, half, l32, bias_pre);
 }
 
 // ---------------------------------------------------------------------------
