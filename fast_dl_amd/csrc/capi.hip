@@ -223,31 +223,6 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
     const int64_t B = batch, I = in_features, Hd = hidden, Cc = classes;
     const hipStream_t hs = as_stream(stream);
     int st;
-    // Forward: H = relu(X W1 + b1), logits = H W2 + b2.
-    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Hd, I, X, I, 0, W1, Hd, 0, H, Hd, 0, 1, b1,
-                      nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
-    if (st) return st;
-    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Cc, Hd, H, Hd, 0, W2, Cc, 0, logits, Cc, 0, 1,
-                      b2, nullptr, FDL_EPILOGUE_BIAS, stream);
-    if (st) return st;
-    // Loss, G2 = dL/dlogits, db2 = colsum(G2) and b2 -= lr * db2 in one kernel
-    // (two launches when the class count is too large to stage in LDS).
-    if (Cc <= fdl::kXentFusedMaxClasses) {
-        st = check_hip(fdl::launch_softmax_xent_db_sgd(logits, labels, loss, G2, db2, b2, lr, B,
-                                                       Cc, hs),
-                       "mlp2_train_step loss failed");
-        if (st) return st;
-    } else {
-        st = fdl_softmax_xent(logits, labels, loss, G2, B, Cc, stream);
-        if (st) return st;
-        st = check_hip(fdl::launch_colsum_sgd(G2, db2, b2, lr, B, Cc, hs),
-                       "mlp2_train_step db2 failed");
-        if (st) return st;
-    }
-    // The backward pass runs as three grouped launches, each holding two
-    // independent jobs.  Updates are ordered after every read of the old
-    // value: W2 is read by the G1 GEMM (launch 1) and updated in launch 3, W1
-    // is read by the dX GEMM (launch 2) and updated in launch 3.
     auto gemm_job = [&](bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float* A,
                         int64_t lda, const float* Bm, int64_t ldb, float* C, int epi,
                         const float* aux, float* upd) {
@@ -270,8 +245,99 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
         j.p.epilogue = epi;
         return j;
     };
-    // Launch 1: G1 = (G2 W2^T) masked by H > 0 (NT, ReLU-gradient epilogue)
-    // and dW2 = H^T G2 (TN).
+    fdl::GroupJob db1_job;  // db1 = colsum(G1), b1 -= lr * db1
+    db1_job.kind = fdl::GroupJob::kColsumSgd;
+    db1_job.x = G1;
+    db1_job.out = db1;
+    db1_job.param = b1;
+    db1_job.lr = lr;
+    db1_job.rows = B;
+    db1_job.cols = Hd;
+    fdl::GroupJob w2_job;  // W2 -= lr * dW2
+    w2_job.kind = fdl::GroupJob::kSgd;
+    w2_job.x = dW2;
+    w2_job.param = W2;
+    w2_job.lr = lr;
+    w2_job.rows = Hd * Cc;
+    // The last launch of either sequence: dW1 = X^T G1 (TN) with W1 -= lr * dW1
+    // in the epilogue, and W2 -= lr * dW2.
+    auto last_launch = [&]() {
+        return check_hip(fdl::launch_group2(gemm_job(true, false, I, Hd, B, X, I, G1, Hd, dW1,
+                                                     fdl::EPI_SGD, nullptr, W1),
+                                            w2_job, hs),
+                         "mlp2_train_step dW1/W2 failed");
+    };
+
+    // Forward layer 1: H = relu(X W1 + b1).
+    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Hd, I, X, I, 0, W1, Hd, 0, H, Hd, 0, 1, b1,
+                      nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
+    if (st) return st;
+
+    // Four launches when the head fits one block per kHeadRows rows (W2 in
+    // LDS) and its per-block records fit in dW1, which holds them until the
+    // last launch overwrites it with the weight gradient.  Every parameter is
+    // updated in a later launch than its last read: b2 and W2 are read by the
+    // head (launch 2), b2 is updated in launch 3 and W2 in launch 4; b1 is
+    // read by launch 1 and updated in launch 3; W1 is read by launch 1 and by
+    // the dX product (launch 3) and updated in launch 4.
+    const int64_t records = fdl::head_blocks(B);
+    const bool fused_head = fdl::head_supported(Hd, Cc) && records * (Cc + 1) <= I * Hd;
+    if (fused_head) {
+        // Launch 2: logits, loss shares, G2 and G1 = (G2 W2^T) * [H > 0].
+        st = check_hip(fdl::launch_mlp_head(H, W2, b2, labels, logits, G2, G1, dW1, B, Hd, Cc,
+                                            hs),
+                       "mlp2_train_step head failed");
+        if (st) return st;
+        // Launch 3: dX = G1 W1^T (NT), db1 with the b1 step, dW2 = H^T G2
+        // (TN), and the records' reduction into loss, db2 and the b2 step.
+        fdl::GroupJob fin;
+        fin.kind = fdl::GroupJob::kXentFinalize;
+        fin.x = dW1;
+        fin.out = db2;
+        fin.out2 = loss;
+        fin.param = b2;
+        fin.lr = lr;
+        fin.rows = records;
+        fin.cols = Cc;
+        const fdl::GroupJob dw2_job = gemm_job(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2,
+                                               fdl::EPI_NONE, nullptr, nullptr);
+        if (dX) {
+            const fdl::GroupJob jobs[4] = {gemm_job(false, true, B, I, Hd, G1, Hd, W1, Hd, dX,
+                                                    fdl::EPI_NONE, nullptr, nullptr),
+                                           db1_job, dw2_job, fin};
+            st = check_hip(fdl::launch_group(jobs, 4, hs), "mlp2_train_step backward failed");
+        } else {
+            const fdl::GroupJob jobs[3] = {db1_job, dw2_job, fin};
+            st = check_hip(fdl::launch_group(jobs, 3, hs), "mlp2_train_step backward failed");
+        }
+        if (st) return st;
+        return last_launch();
+    }
+
+    // Otherwise six launches.  logits = H W2 + b2.
+    st = fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, B, Cc, Hd, H, Hd, 0, W2, Cc, 0, logits, Cc, 0, 1,
+                      b2, nullptr, FDL_EPILOGUE_BIAS, stream);
+    if (st) return st;
+    // Loss, G2 = dL/dlogits, db2 = colsum(G2) and b2 -= lr * db2 in one kernel
+    // (two launches when the class count is too large to stage in LDS).
+    if (Cc <= fdl::kXentFusedMaxClasses) {
+        st = check_hip(fdl::launch_softmax_xent_db_sgd(logits, labels, loss, G2, db2, b2, lr, B,
+                                                       Cc, hs),
+                       "mlp2_train_step loss failed");
+        if (st) return st;
+    } else {
+        st = fdl_softmax_xent(logits, labels, loss, G2, B, Cc, stream);
+        if (st) return st;
+        st = check_hip(fdl::launch_colsum_sgd(G2, db2, b2, lr, B, Cc, hs),
+                       "mlp2_train_step db2 failed");
+        if (st) return st;
+    }
+    // The backward pass runs as three grouped launches of independent jobs.
+    // Updates are ordered after every read of the old value: W2 is read by
+    // the G1 GEMM (first launch) and updated in the third, W1 is read by the
+    // dX GEMM (second launch) and updated in the third.
+    // G1 = (G2 W2^T) masked by H > 0 (NT, ReLU-gradient epilogue) and
+    // dW2 = H^T G2 (TN).
     st = check_hip(fdl::launch_group2(
                        gemm_job(false, true, B, Hd, Cc, G2, Cc, W2, Cc, G1,
                                 fdl::EPI_RELU_GRAD, H, nullptr),
@@ -280,15 +346,7 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
                        hs),
                    "mlp2_train_step G1/dW2 failed");
     if (st) return st;
-    // Launch 2: dX = G1 W1^T (NT) and db1 = colsum(G1) with b1 -= lr * db1.
-    fdl::GroupJob db1_job;
-    db1_job.kind = fdl::GroupJob::kColsumSgd;
-    db1_job.x = G1;
-    db1_job.out = db1;
-    db1_job.param = b1;
-    db1_job.lr = lr;
-    db1_job.rows = B;
-    db1_job.cols = Hd;
+    // dX = G1 W1^T (NT) and db1 = colsum(G1) with b1 -= lr * db1.
     if (dX) {
         st = check_hip(fdl::launch_group2(gemm_job(false, true, B, I, Hd, G1, Hd, W1, Hd, dX,
                                                    fdl::EPI_NONE, nullptr, nullptr),
@@ -299,18 +357,7 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
                        "mlp2_train_step db1 failed");
     }
     if (st) return st;
-    // Launch 3: dW1 = X^T G1 (TN) with W1 -= lr * dW1 in the epilogue, and
-    // W2 -= lr * dW2.
-    fdl::GroupJob w2_job;
-    w2_job.kind = fdl::GroupJob::kSgd;
-    w2_job.x = dW2;
-    w2_job.param = W2;
-    w2_job.lr = lr;
-    w2_job.rows = Hd * Cc;
-    return check_hip(fdl::launch_group2(gemm_job(true, false, I, Hd, B, X, I, G1, Hd, dW1,
-                                                 fdl::EPI_SGD, nullptr, W1),
-                                        w2_job, hs),
-                     "mlp2_train_step dW1/W2 failed");
+    return last_launch();
 }
 
 }  // extern "C"

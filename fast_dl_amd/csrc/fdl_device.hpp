@@ -50,6 +50,37 @@ __device__ __forceinline__ void colsum_body(const float* __restrict__ x, float* 
     }
 }
 
+// Final reduction of the MLP head's per-block partials (one block): part holds
+// nparts records of classes + 1 floats, the block's bias-gradient column sums
+// then its loss.  Records are added in block order (deterministic); then
+// db[c] = sum, bparam[c] -= lr * sum, loss[0] = sum of the loss partials.
+__device__ __forceinline__ void xent_finalize_body(const float* __restrict__ part, int nparts,
+                                                   int classes, float* __restrict__ loss,
+                                                   float* __restrict__ db,
+                                                   float* __restrict__ bparam, float lr) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+    if (t > classes) return;
+    const int stride = classes + 1;
+    float s = 0.0f;
+    int b = 0;
+    for (; b + 8 <= nparts; b += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[(b + u) * stride + t];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; b < nparts; ++b) s += part[b * stride + t];
+    if (t < classes) {
+        db[t] = s;
+        const float step = lr * s;
+        bparam[t] = bparam[t] - step;
+    } else if (loss) {
+        loss[0] = s;
+    }
+}
+
 // p[i] -= lr * g[i] over a grid-stride range; the product is rounded before
 // the subtraction (no FMA contraction), as in the reference's host update.
 __device__ __forceinline__ void sgd_body(float* __restrict__ p, const float* __restrict__ g,

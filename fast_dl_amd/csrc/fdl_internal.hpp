@@ -64,25 +64,35 @@ enum class GemmKernel : int {
 bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool transB,
                    int64_t batch);
 
-// One job of a grouped launch (launch_group2): a split-K GEMM (32x32 output
+// One job of a grouped launch (launch_group): a split-K GEMM (32x32 output
 // tiles, four waves per block, any epilogue), a column sum with the bias SGD
-// step, or an SGD update p -= lr * g.
+// step, an SGD update p -= lr * g, or the final reduction of the MLP head's
+// partial records (xent_finalize_body).
 struct GroupJob {
-    enum Kind { kGemm, kColsumSgd, kSgd };
+    enum Kind { kGemm, kColsumSgd, kSgd, kXentFinalize };
     Kind kind = kGemm;
     GemmParams p{};              // kGemm
     bool ta = false, tb = false;
-    const float* x = nullptr;    // kColsumSgd: rows x cols input; kSgd: gradient
-    float* out = nullptr;        // kColsumSgd: column sums
-    float* param = nullptr;      // kColsumSgd, kSgd: the parameter updated
+    const float* x = nullptr;    // kColsumSgd: rows x cols input; kSgd: gradient;
+                                 // kXentFinalize: the partial records
+    float* out = nullptr;        // kColsumSgd, kXentFinalize: column sums (db)
+    float* out2 = nullptr;       // kXentFinalize: loss
+    float* param = nullptr;      // kColsumSgd, kSgd, kXentFinalize: the parameter updated
     float lr = 0.0f;
-    int64_t rows = 0, cols = 0;  // kSgd: rows is the element count
+    int64_t rows = 0, cols = 0;  // kSgd: rows is the element count;
+                                 // kXentFinalize: records, classes
 };
 
-// Runs two independent jobs in one launch, job 0 on the first blocks of the
-// grid.  Supported pairs are the ones the MLP step uses: (NT GEMM, TN GEMM),
-// (NT GEMM, column sum), (TN GEMM, SGD); others return hipErrorInvalidValue.
-hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream);
+// Runs n (2 to 4) independent jobs in one launch, job 0 on the first blocks
+// of the grid.  Supported sequences are the ones the MLP step uses:
+// (NT GEMM, TN GEMM), (NT GEMM, column sum), (TN GEMM, SGD),
+// (NT GEMM, column sum, TN GEMM, finalize) and (column sum, TN GEMM,
+// finalize); others return hipErrorInvalidValue.
+hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream);
+inline hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream) {
+    const GroupJob jobs[2] = {j0, j1};
+    return launch_group(jobs, 2, stream);
+}
 
 // Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
 hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,
@@ -119,6 +129,23 @@ hipError_t launch_softmax_xent_db_sgd(const float* logits, const int64_t* labels
                                       float* loss, float* grad, float* db, float* bparam,
                                       float lr, int64_t batch, int64_t classes,
                                       hipStream_t stream);
+// The MLP step's head, kHeadRows rows per block: logits = H W2 + b2, loss
+// and G2 = dL/dlogits as launch_softmax_xent, G1 = (G2 W2^T) * [H > 0], and
+// each block's partial record (column sums of its G2 rows, then its loss
+// share) at part + block * (classes + 1).  xent_finalize_body reduces the
+// records.  W2 is staged in LDS with rows padded to 16 or 32 classes, which
+// bounds the shapes: classes <= 16 with hidden <= 1024, or classes <= 32
+// with hidden <= 512.
+constexpr int kHeadRows = 8;
+inline bool head_supported(int64_t hidden, int64_t classes) {
+    return hidden >= 1 && classes >= 1 &&
+           ((classes <= 16 && hidden <= 1024) || (classes <= 32 && hidden <= 512));
+}
+inline int64_t head_blocks(int64_t batch) { return (batch + kHeadRows - 1) / kHeadRows; }
+hipError_t launch_mlp_head(const float* H, const float* W2, const float* b2,
+                           const int64_t* labels, float* logits, float* G2, float* G1,
+                           float* part, int64_t batch, int64_t hidden, int64_t classes,
+                           hipStream_t stream);
 hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,
                       hipStream_t stream);
 // Up to four (param, grad, n) updates in one launch.

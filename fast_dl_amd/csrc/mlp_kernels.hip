@@ -19,6 +19,28 @@ inline unsigned grid_for(int64_t n, int per_thread = 1) {
     return (unsigned)std::min<int64_t>(blocks, 1 << 20);
 }
 
+// dst[e] = src[e] for e < n by a block of kBlock threads, 16 loads in flight
+// per thread before their LDS stores (a plain strided loop waits out one
+// global-memory round trip per iteration).
+__device__ __forceinline__ void stage_to_lds(float* __restrict__ dst, const float* __restrict__ src,
+                                             int n) {
+    constexpr int kBatch = 16;
+    const int t = threadIdx.x;
+    for (int e0 = 0; e0 < n; e0 += kBatch * kBlock) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int e = e0 + u * kBlock + t;
+            v[u] = e < n ? src[e] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int e = e0 + u * kBlock + t;
+            if (e < n) dst[e] = v[u];
+        }
+    }
+}
+
 // out[r, c] += bias[c]   (src/kernels/cuda/bias.cu:5-12 semantics)
 __global__ void add_row_bias_kernel(float* __restrict__ out,
                                     const float* __restrict__ bias,
@@ -153,8 +175,7 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
         const int rows = (int)min<int64_t>(kBlock, batch - r0);
         const int n = rows * (int)classes;
         const int64_t label = t < rows ? labels[r0 + t] : -1;
-        const float* zsrc = logits + r0 * classes;
-        for (int e = t; e < n; e += kBlock) zs[e] = zsrc[e];
+        stage_to_lds(zs, logits + r0 * classes, n);
         __syncthreads();
         if (t < rows) {
             float* z = zs + t * classes;
@@ -196,6 +217,179 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
         float l = wpart[0];
         for (int w = 1; w < kBlock / 64; ++w) l += wpart[w];
         loss[0] = l;
+    }
+}
+
+// The MLP step's head: kHeadRows rows per block, one half-wave (32 lanes) per
+// row; CM >= classes and 32 * NH >= hidden are compile-time bounds.  Lane l
+// holds H[row][l + 32 k].  W2 is staged in LDS as 32 * NH rows of CM floats
+// (row stride CM + 4), zero past `hidden` rows and `classes` columns, so every loop over classes
+// runs to CM with no bounds test (the padding adds exact zeros) and its LDS
+// reads are issued together.
+//   logits[row][c] = sum_j H[row][j] W2[j][c] + b2[c]: the 32 lane partials
+//     meet in an xor butterfly, so every lane of the row ends with the same
+//     sums; the bias is added after the sum, as in linear_cpu
+//     (tests/tensor/linear_tensor_test.cpp:17-25).
+//   loss share and G2[row][c] as in softmax_xent_db_sgd_kernel (the legacy
+//     SoftmaxCrossEntropyLoss forward and backward,
+//     legacy/src/ops/SoftmaxCrossEntropyLoss.cpp:39-51).
+//   G1[row][j] = H[row][j] > 0 ? sum_c G2[row][c] W2[j][c] : 0 (the NT product
+//     dY1 = G2 W2^T of legacy/src/ops/Layers.cpp:36 through the ReLU mask).
+// The block's record at part + block * (classes + 1): the column sums of its
+// G2 rows (rows in order), then the sum of its rows' loss shares;
+// xent_finalize_body adds the records in block order.
+// Sum over the 32 lanes of a half-wave; every lane gets the same value (each
+// step adds the same two operands on both lanes of a pair, in either order).
+// Lanes are paired by quad permutations, then the 8- and 16-lane mirrors
+// (which pair the groups made uniform by the steps before), then xor 16.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                 kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float half_wave_sum(float v) {
+    constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1, 0, 3, 2]
+    constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2, 3, 0, 1]
+    constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7 - i of each 8
+    constexpr int kMirror = 0x140;      // row_mirror: lane i <-> 15 - i of each 16
+    constexpr int kXor16 = 0x401F;      // ds_swizzle bit mode: and 0x1f, xor 0x10
+    v += dpp_mov<kQuadSwap1>(v);
+    v += dpp_mov<kQuadSwap2>(v);
+    v += dpp_mov<kHalfMirror>(v);
+    v += dpp_mov<kMirror>(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), kXor16));
+    return v;
+}
+
+template <int CM, int NH>
+__global__ void __launch_bounds__(kBlock)
+mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
+                const float* __restrict__ b2, const int64_t* __restrict__ labels,
+                float* __restrict__ logits, float* __restrict__ G2, float* __restrict__ G1,
+                float* __restrict__ part, int batch, int hidden, int classes) {
+    constexpr int JR = 32 * NH;                  // W2 rows staged
+    constexpr int LR = CM + 4;                   // LDS row stride: 16 consecutive lanes
+                                                 // read 16-byte pieces on distinct banks
+    constexpr int kPerThread = JR * CM / kBlock;  // staged floats per thread
+    static_assert(kPerThread % 16 == 0, "staging runs in batches of 16 loads");
+    __shared__ __attribute__((aligned(16))) float w2s[JR * LR];
+    __shared__ float b2s[CM];
+    __shared__ float g2s[kHeadRows][CM];
+    __shared__ float ls[kHeadRows];
+    const int t = threadIdx.x;
+    const int lane = t & 31;
+    const int rl = t >> 5;
+    const int row = blockIdx.x * kHeadRows + rl;
+    const bool live = row < batch;
+    const int rowc = live ? row : batch - 1;  // clamped: loads stay in bounds
+    const int64_t label = labels[rowc];
+    const float* hrow = H + (int64_t)rowc * hidden;
+    float h[NH];
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+        const int j = lane + 32 * k;
+        h[k] = j < hidden ? hrow[j] : 0.0f;
+    }
+    b2s[t % CM] = (t % CM) < classes ? b2[t % CM] : 0.0f;
+    // Sixteen loads in flight per thread before their LDS stores.
+#pragma unroll
+    for (int b0 = 0; b0 < kPerThread; b0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int e = (b0 + u) * kBlock + t;
+            const int j = e / CM, c = e % CM;
+            v[u] = (j < hidden && c < classes) ? W2[j * classes + c] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int e = (b0 + u) * kBlock + t;
+            w2s[(e / CM) * LR + e % CM] = v[u];
+        }
+    }
+    __syncthreads();
+
+    float z[CM];
+#pragma unroll
+    for (int c = 0; c < CM; ++c) z[c] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+        const float* w = w2s + (lane + 32 * k) * LR;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) z[c] = fmaf(h[k], w[c], z[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < CM; ++c) z[c] = half_wave_sum(z[c]);
+
+    float g[CM];
+    float loss_share = 0.0f;
+    {
+#pragma clang fp contract(off)
+        const float inv_b = 1.0f / (float)batch;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) z[c] = z[c] + b2s[c];
+        float mx = z[0];
+#pragma unroll
+        for (int c = 1; c < CM; ++c) mx = c < classes ? fmaxf(mx, z[c]) : mx;
+        float s = 0.0f;
+        float ez[CM];
+#pragma unroll
+        for (int c = 0; c < CM; ++c) {
+            ez[c] = c < classes ? expf(z[c] - mx) : 0.0f;
+            s += c < classes ? ez[c] : 0.0f;
+        }
+        const bool valid = label >= 0 && label < classes;
+        float zl = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) zl = c == label ? z[c] : zl;
+        if (valid && live) loss_share = (logf(s) + mx - zl) * inv_b;
+        const float inv_s = 1.0f / s;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) {
+            float pc = c < classes ? ez[c] * inv_s : 0.0f;
+            if (valid && c == label) pc -= 1.0f;
+            g[c] = pc * inv_b;
+        }
+    }
+    // Lane c writes class c of the row.
+    float zsel = 0.0f, gsel = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CM; ++c) {
+        zsel = c == lane ? z[c] : zsel;
+        gsel = c == lane ? g[c] : gsel;
+    }
+    if (lane < classes) {
+        if (live) {
+            logits[(int64_t)row * classes + lane] = zsel;
+            G2[(int64_t)row * classes + lane] = gsel;
+        }
+        g2s[rl][lane] = live ? gsel : 0.0f;
+    }
+    if (lane == 0) ls[rl] = loss_share;
+
+    float* g1row = G1 + (int64_t)rowc * hidden;
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+        const int j = lane + 32 * k;
+        const float* w = w2s + j * LR;
+        float v = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) v = fmaf(g[c], w[c], v);
+        if (live && j < hidden) g1row[j] = h[k] > 0.0f ? v : 0.0f;
+    }
+    __syncthreads();
+    if (t <= classes) {
+#pragma clang fp contract(off)
+        float acc = 0.0f;
+        if (t < classes) {
+#pragma unroll
+            for (int r = 0; r < kHeadRows; ++r) acc += g2s[r][t];
+        } else {
+#pragma unroll
+            for (int r = 0; r < kHeadRows; ++r) acc += ls[r];
+        }
+        part[(int64_t)blockIdx.x * (classes + 1) + t] = acc;
     }
 }
 
@@ -349,6 +543,36 @@ hipError_t launch_softmax_xent_db_sgd(const float* logits, const int64_t* labels
     hipLaunchKernelGGL(softmax_xent_db_sgd_kernel, dim3(1), dim3(kBlock), 0, stream, logits,
                        labels, loss, grad, db, bparam, lr, batch, classes);
     return hipGetLastError();
+}
+
+template <int CM, int NH>
+hipError_t launch_mlp_head_cfg(const float* H, const float* W2, const float* b2,
+                               const int64_t* labels, float* logits, float* G2, float* G1,
+                               float* part, int64_t batch, int64_t hidden, int64_t classes,
+                               hipStream_t stream) {
+    hipLaunchKernelGGL((mlp_head_kernel<CM, NH>), dim3((unsigned)head_blocks(batch)),
+                       dim3(kBlock), 0, stream, H, W2, b2, labels, logits, G2, G1, part,
+                       (int)batch, (int)hidden, (int)classes);
+    return hipGetLastError();
+}
+
+hipError_t launch_mlp_head(const float* H, const float* W2, const float* b2,
+                           const int64_t* labels, float* logits, float* G2, float* G1,
+                           float* part, int64_t batch, int64_t hidden, int64_t classes,
+                           hipStream_t stream) {
+    if (!head_supported(hidden, classes) || batch < 1 || batch > INT32_MAX) {
+        return hipErrorInvalidValue;
+    }
+    if (classes <= 16) {
+        return hidden <= 256 ? launch_mlp_head_cfg<16, 8>(H, W2, b2, labels, logits, G2, G1,
+                                                          part, batch, hidden, classes, stream)
+                             : launch_mlp_head_cfg<16, 32>(H, W2, b2, labels, logits, G2, G1,
+                                                           part, batch, hidden, classes, stream);
+    }
+    return hidden <= 256 ? launch_mlp_head_cfg<32, 8>(H, W2, b2, labels, logits, G2, G1, part,
+                                                      batch, hidden, classes, stream)
+                         : launch_mlp_head_cfg<32, 16>(H, W2, b2, labels, logits, G2, G1, part,
+                                                       batch, hidden, classes, stream);
 }
 
 hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,

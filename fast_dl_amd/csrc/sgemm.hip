@@ -1578,18 +1578,25 @@ hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
 }
 
 // ---------------------------------------------------------------------------
-// Grouped launches: two independent jobs in one grid, so that dependent
-// chains of small kernels (the MLP step's backward pass) pay one launch for
-// two jobs.  Every job body runs on 256 threads.
+// Grouped launches: up to four independent jobs in one grid, so that
+// dependent chains of small kernels (the MLP step's backward pass) pay one
+// launch for several jobs.  Every job body runs on 256 threads.
 // ---------------------------------------------------------------------------
 struct GroupDev {
     GemmParams p;
     int tiles_m, tiles_n, kchunk, blocks;
     const float* x;
     float* out;
+    float* out2;
     float* param;
     float lr;
     int64_t rows, cols;
+};
+
+constexpr int kGroupMaxJobs = 4;
+
+struct GroupArgs {
+    GroupDev d[kGroupMaxJobs];
 };
 
 constexpr int kGroupKW = 4;   // split-K waves of a grouped GEMM job (256 threads)
@@ -1615,14 +1622,32 @@ struct JobSgd {
     }
 };
 
-template <class J0, class J1>
-__global__ void __launch_bounds__(kGroupKW * kWave)
-sgemm_group_kernel(GroupDev a0, GroupDev a1) {
-    if ((int)blockIdx.x < a0.blocks) {
-        J0::run(a0, blockIdx.x);
-    } else {
-        J1::run(a1, (int)blockIdx.x - a0.blocks);
+struct JobXentFinalize {
+    static __device__ __forceinline__ void run(const GroupDev& a, int) {
+        xent_finalize_body(a.x, (int)a.rows, (int)a.cols, a.out2, a.out, a.param, a.lr);
     }
+};
+
+// Block `bid` of the grid runs job I if it falls in that job's range, else
+// the next job with the index rebased.
+template <int I, class J, class... Rest>
+__device__ __forceinline__ void group_dispatch(const GroupArgs& a, int bid) {
+    if constexpr (sizeof...(Rest) == 0) {
+        J::run(a.d[I], bid);
+    } else {
+        if (bid < a.d[I].blocks) {
+            J::run(a.d[I], bid);
+        } else {
+            group_dispatch<I + 1, Rest...>(a, bid - a.d[I].blocks);
+        }
+    }
+}
+
+template <class... J>
+__global__ void __launch_bounds__(kGroupKW * kWave)
+sgemm_group_kernel(GroupArgs a) {
+    static_assert(sizeof...(J) >= 2 && sizeof...(J) <= kGroupMaxJobs, "2 to 4 jobs");
+    group_dispatch<0, J...>(a, blockIdx.x);
 }
 
 template <int KW, int ITS = 1>
@@ -1893,6 +1918,7 @@ GroupDev group_dev(const GroupJob& j) {
     d.p = j.p;
     d.x = j.x;
     d.out = j.out;
+    d.out2 = j.out2;
     d.param = j.param;
     d.lr = j.lr;
     d.rows = j.rows;
@@ -1913,49 +1939,69 @@ GroupDev group_dev(const GroupJob& j) {
         case GroupJob::kSgd:
             d.blocks = (int)std::min<int64_t>((j.rows + 4 * 256 - 1) / (4 * 256), 1024);
             break;
+        case GroupJob::kXentFinalize:
+            d.blocks = 1;
+            break;
     }
     return d;
 }
 
-template <class J0, class J1>
-hipError_t launch_group_pair(const GroupDev& a0, const GroupDev& a1, hipStream_t stream) {
-    hipLaunchKernelGGL((sgemm_group_kernel<J0, J1>), dim3(a0.blocks + a1.blocks),
-                       dim3(kGroupKW * kWave), 0, stream, a0, a1);
+template <class... J>
+hipError_t launch_group_of(const GroupArgs& a, hipStream_t stream) {
+    int blocks = 0;
+    for (int i = 0; i < (int)sizeof...(J); ++i) blocks += a.d[i].blocks;
+    hipLaunchKernelGGL((sgemm_group_kernel<J...>), dim3(blocks), dim3(kGroupKW * kWave), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
-// Vector flags of an NT GEMM job (A and B both k-contiguous), as launch_sgemm
-// derives them.
-template <class J1>
-hipError_t launch_nt_then(const GroupJob& j0, const GroupDev& a0, const GroupDev& a1,
-                          hipStream_t stream) {
+// The NT GEMM job with the vector flags launch_sgemm would derive for it (A
+// and B both k-contiguous), followed by the jobs Rest.
+template <class... Rest>
+hipError_t launch_nt_first(const GroupJob& j0, const GroupArgs& a, hipStream_t stream) {
     const bool va = vec_ok(j0.p.A, j0.p.K, j0.p.lda, j0.p.strideA, 1);
     const bool vb = vec_ok(j0.p.B, j0.p.K, j0.p.ldb, j0.p.strideB, 1);
-    if (va && vb) return launch_group_pair<JobGemm<false, true, true, true>, J1>(a0, a1, stream);
-    if (va) return launch_group_pair<JobGemm<false, true, true, false>, J1>(a0, a1, stream);
-    if (vb) return launch_group_pair<JobGemm<false, true, false, true>, J1>(a0, a1, stream);
-    return launch_group_pair<JobGemm<false, true, false, false>, J1>(a0, a1, stream);
+    if (va && vb) return launch_group_of<JobGemm<false, true, true, true>, Rest...>(a, stream);
+    if (va) return launch_group_of<JobGemm<false, true, true, false>, Rest...>(a, stream);
+    if (vb) return launch_group_of<JobGemm<false, true, false, true>, Rest...>(a, stream);
+    return launch_group_of<JobGemm<false, true, false, false>, Rest...>(a, stream);
 }
 
 }  // namespace
 
-hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream) {
-    const bool nt0 = j0.kind == GroupJob::kGemm && !j0.ta && j0.tb;
-    const bool tn0 = j0.kind == GroupJob::kGemm && j0.ta && !j0.tb;
-    const bool tn1 = j1.kind == GroupJob::kGemm && j1.ta && !j1.tb;
-    for (const GroupJob* j : {&j0, &j1}) {
-        if (j->kind == GroupJob::kGemm && (j->p.M <= 0 || j->p.N <= 0 || j->p.K <= 0)) {
+hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
+    if (n < 2 || n > kGroupMaxJobs) return hipErrorInvalidValue;
+    GroupArgs a{};
+    for (int i = 0; i < n; ++i) {
+        const GroupJob& j = jobs[i];
+        if (j.kind == GroupJob::kGemm && (j.p.M <= 0 || j.p.N <= 0 || j.p.K <= 0)) {
             return hipErrorInvalidValue;
         }
+        a.d[i] = group_dev(j);
     }
-    const GroupDev a0 = group_dev(j0);
-    const GroupDev a1 = group_dev(j1);
-    if (nt0 && tn1) return launch_nt_then<JobGemm<true, false, false, false>>(j0, a0, a1, stream);
-    if (nt0 && j1.kind == GroupJob::kColsumSgd) {
-        return launch_nt_then<JobColsumSgd>(j0, a0, a1, stream);
-    }
-    if (tn0 && j1.kind == GroupJob::kSgd) {
-        return launch_group_pair<JobGemm<true, false, false, false>, JobSgd>(a0, a1, stream);
+    auto is_nt = [&](int i) {
+        return jobs[i].kind == GroupJob::kGemm && !jobs[i].ta && jobs[i].tb;
+    };
+    auto is_tn = [&](int i) {
+        return jobs[i].kind == GroupJob::kGemm && jobs[i].ta && !jobs[i].tb;
+    };
+    auto is = [&](int i, GroupJob::Kind k) { return jobs[i].kind == k; };
+    using TN = JobGemm<true, false, false, false>;
+    if (n == 2) {
+        if (is_nt(0) && is_tn(1)) return launch_nt_first<TN>(jobs[0], a, stream);
+        if (is_nt(0) && is(1, GroupJob::kColsumSgd)) {
+            return launch_nt_first<JobColsumSgd>(jobs[0], a, stream);
+        }
+        if (is_tn(0) && is(1, GroupJob::kSgd)) return launch_group_of<TN, JobSgd>(a, stream);
+    } else if (n == 3) {
+        if (is(0, GroupJob::kColsumSgd) && is_tn(1) && is(2, GroupJob::kXentFinalize)) {
+            return launch_group_of<JobColsumSgd, TN, JobXentFinalize>(a, stream);
+        }
+    } else {
+        if (is_nt(0) && is(1, GroupJob::kColsumSgd) && is_tn(2) &&
+            is(3, GroupJob::kXentFinalize)) {
+            return launch_nt_first<JobColsumSgd, TN, JobXentFinalize>(jobs[0], a, stream);
+        }
     }
     return hipErrorInvalidValue;
 }

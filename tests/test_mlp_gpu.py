@@ -199,10 +199,16 @@ def test_mlp_config2_step(device):
     assert losses[-1] < losses[0]
 
 
-@pytest.mark.parametrize("B,I,H,C", [(300, 50, 20, 10), (64, 30, 17, 40), (1, 8, 4, 3)])
+@pytest.mark.parametrize("B,I,H,C", [(300, 50, 20, 10), (1, 8, 4, 3), (17, 9, 256, 16),
+                                     (24, 6, 1000, 12), (260, 12, 300, 20), (64, 30, 17, 40),
+                                     (16, 8, 1100, 5), (10, 5, 600, 20), (64, 1, 2, 10)])
 def test_mlp_step_shapes(device, B, I, H, C):
-    # batch beyond one 256-row chunk of the fused loss kernel, a class count past
-    # its LDS staging limit (separate loss and bias-gradient kernels), batch 1
+    # Four-launch step (head kernel): a batch that is not a multiple of the
+    # head's 8 rows per block, batch 1, up to 16 classes with hidden up to 256
+    # and up to 1024, up to 32 classes with hidden up to 512.  Six-launch
+    # step: a class count past 32 (separate loss and bias-gradient kernels),
+    # hidden past 1024, 17-32 classes with hidden past 512, and a dW1 too
+    # small to hold the head's per-block records.
     g = rng(B * 7 + C)
     X = g.random((B, I)).astype(np.float32)
     labels = g.integers(0, C, B).astype(np.int64)
