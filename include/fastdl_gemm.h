@@ -214,6 +214,11 @@ int fdl_sgd_update(float* param, const float* grad, float lr, int64_t n,
  *
  * Every buffer belongs to the caller; the step allocates nothing.  H, logits,
  * G2, G1, dW1, db1, dW2, db2 hold the step's intermediates on return.
+ * The step is 4 launches when classes <= 16 and hidden <= 1024, or
+ * classes <= 32 and hidden <= 512, and ceil(batch / 8) * (classes + 1) <=
+ * in_features * hidden: then dW1 holds per-block partial sums of the loss
+ * and db2 until the last launch writes the weight gradient into it.
+ * Otherwise it is 6 launches.
  */
 int fdl_mlp2_train_step(const float* X, const int64_t* labels,
                         int64_t batch, int64_t in_features,
