@@ -1,15 +1,19 @@
-// dl:: value types (Device, DType, Shape) and HIP error checks.
+// dl:: value types (Device, DType, Shape), streams and HIP error checks.
 // Behaviour follows src/core/{Device,DType,Shape,CudaUtils}.cpp of the reference.
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
 #include <dl/core/HipUtils.hpp>
 #include <dl/core/Shape.hpp>
+#include <dl/core/Stream.hpp>
 
 #include <fastdl_gemm.h>
+
+#include <hip/hip_runtime_api.h>
 
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 namespace dl {
 
@@ -64,6 +68,53 @@ std::string Shape::str() const {
     for (std::size_t i = 0; i < dims.size(); ++i) os << (i ? ", " : "") << dims[i];
     os << ")";
     return os.str();
+}
+
+// ------------------------------------------------------------------ streams
+
+namespace {
+
+thread_local void* t_current_stream = nullptr;
+
+}  // namespace
+
+Stream::Stream(const Device& device) {
+    if (!device.is_cuda()) throw std::runtime_error("Stream: device must be a GPU");
+    hip::check(hipSetDevice(device.index), "cudaSetDevice failed");
+    hipStream_t s = nullptr;
+    hip::check(hipStreamCreate(&s), "stream create failed");
+    stream_ = s;
+}
+
+Stream::~Stream() {
+    if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+}
+
+Stream::Stream(Stream&& other) noexcept : stream_(std::exchange(other.stream_, nullptr)) {}
+
+Stream& Stream::operator=(Stream&& other) noexcept {
+    if (this != &other) {
+        if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+        stream_ = std::exchange(other.stream_, nullptr);
+    }
+    return *this;
+}
+
+void Stream::synchronize() const {
+    hip::check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "stream synchronize failed");
+}
+
+void* current_stream() { return t_current_stream; }
+
+void set_current_stream(void* stream) { t_current_stream = stream; }
+
+StreamGuard::StreamGuard(void* stream) : previous_(t_current_stream) { t_current_stream = stream; }
+
+StreamGuard::~StreamGuard() { t_current_stream = previous_; }
+
+void synchronize() {
+    hip::check(hipStreamSynchronize(static_cast<hipStream_t>(t_current_stream)),
+               "stream synchronize failed");
 }
 
 namespace hip {

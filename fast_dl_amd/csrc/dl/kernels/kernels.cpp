@@ -3,6 +3,7 @@
 // reference) onto this build's gfx950 kernels and turns a non-zero status
 // into std::runtime_error.
 #include <dl/core/HipUtils.hpp>
+#include <dl/core/Stream.hpp>
 #include <dl/kernels/kernels.hpp>
 
 #include <fastdl_gemm.h>
@@ -63,7 +64,7 @@ int epilogue_id(Epilogue e) {
 
 void gemm(const float* a, const float* b, float* c, int m, int n, int k, GemmAlgo algo) {
     gemm_ex(Transpose::No, Transpose::No, m, n, k, a, k > 0 ? k : 1, 0, b, n > 0 ? n : 1, 0, c,
-            n > 0 ? n : 1, 0, 1, nullptr, nullptr, Epilogue::None, algo, nullptr);
+            n > 0 ? n : 1, 0, 1, nullptr, nullptr, Epilogue::None, algo, current_stream());
 }
 
 void gemm_ex(Transpose trans_a, Transpose trans_b, int64_t m, int64_t n, int64_t k,
@@ -80,7 +81,7 @@ void gemm_ex(Transpose trans_a, Transpose trans_b, int64_t m, int64_t n, int64_t
 }
 
 void add_row_bias(float* output, const float* bias, int rows, int cols) {
-    hip::check_fdl(fdl_add_row_bias(output, bias, rows, cols, nullptr), "add_row_bias failed");
+    hip::check_fdl(fdl_add_row_bias(output, bias, rows, cols, current_stream()), "add_row_bias failed");
 }
 
 const char* to_string(ActivationOp op) {
@@ -99,11 +100,11 @@ void activation(const float* a, float* b, int n, ActivationOp op, float /*alpha*
         throw std::runtime_error(std::string("activation '") + to_string(op) +
                                  "' is not provided by this build (only relu is on the GEMM path)");
     }
-    hip::check_fdl(fdl_relu(a, b, n, nullptr), "relu failed");
+    hip::check_fdl(fdl_relu(a, b, n, current_stream()), "relu failed");
 }
 
 void relu_backward(const float* grad_out, const float* act, float* grad_in, int64_t n) {
-    hip::check_fdl(fdl_relu_backward(grad_out, act, grad_in, n, nullptr), "relu_backward failed");
+    hip::check_fdl(fdl_relu_backward(grad_out, act, grad_in, n, current_stream()), "relu_backward failed");
 }
 
 const char* to_string(SoftmaxAlgo algo) {
@@ -118,38 +119,38 @@ const char* to_string(SoftmaxAlgo algo) {
 void softmax(const float* input, float* output, std::size_t rows, std::size_t cols,
              SoftmaxAlgo /*algo*/) {
     hip::check_fdl(fdl_softmax(input, output, static_cast<int64_t>(rows),
-                               static_cast<int64_t>(cols), nullptr),
+                               static_cast<int64_t>(cols), current_stream()),
                    "softmax failed");
 }
 
 void cross_entropy(const float* logits, const int64_t* labels, float* loss, int batch,
                    int classes) {
-    hip::check_fdl(fdl_softmax_xent(logits, labels, loss, nullptr, batch, classes, nullptr),
+    hip::check_fdl(fdl_softmax_xent(logits, labels, loss, nullptr, batch, classes, current_stream()),
                    "cross_entropy failed");
 }
 
 void cross_entropy_backward(const float* logits, const int64_t* labels, float* loss,
                             float* grad, int batch, int classes) {
-    hip::check_fdl(fdl_softmax_xent(logits, labels, loss, grad, batch, classes, nullptr),
+    hip::check_fdl(fdl_softmax_xent(logits, labels, loss, grad, batch, classes, current_stream()),
                    "cross_entropy_backward failed");
 }
 
 void uniform_float32(float* data, int64_t n, float low, float high, uint64_t seed) {
     if (n <= 0) return;
-    hip::check_fdl(fdl_fill_uniform(data, n, low, high, seed, nullptr), "uniform fill failed");
+    hip::check_fdl(fdl_fill_uniform(data, n, low, high, seed, current_stream()), "uniform fill failed");
 }
 
 void normal_float32(float* data, int64_t n, float mean, float stddev, uint64_t seed) {
     if (n <= 0) return;
-    hip::check_fdl(fdl_fill_normal(data, n, mean, stddev, seed, nullptr), "normal fill failed");
+    hip::check_fdl(fdl_fill_normal(data, n, mean, stddev, seed, current_stream()), "normal fill failed");
 }
 
 void colsum(const float* x, float* out, int64_t rows, int64_t cols) {
-    hip::check_fdl(fdl_colsum(x, out, rows, cols, nullptr), "colsum failed");
+    hip::check_fdl(fdl_colsum(x, out, rows, cols, current_stream()), "colsum failed");
 }
 
 void sgd_update(float* param, const float* grad, float lr, int64_t n) {
-    hip::check_fdl(fdl_sgd_update(param, grad, lr, n, nullptr), "sgd_update failed");
+    hip::check_fdl(fdl_sgd_update(param, grad, lr, n, current_stream()), "sgd_update failed");
 }
 
 }  // namespace dl::kernels

@@ -4,6 +4,7 @@
 // compute differs: linear's bias is fused into the GEMM epilogue instead of a
 // second pass over the output.
 #include <dl/core/HipUtils.hpp>
+#include <dl/core/Stream.hpp>
 #include <dl/kernels/kernels.hpp>
 #include <dl/ops/Ops.hpp>
 #include <dl/ops/OpUtils.hpp>
@@ -105,7 +106,7 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
     Tensor out(Shape({m, n}), a.dtype(), a.device());
     set_device(a);
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, m, n, k, f32(a), k, 0, f32(b), n, 0,
-                                f32(out), n, 0, 1, nullptr, nullptr, FDL_EPILOGUE_NONE, nullptr),
+                                f32(out), n, 0, 1, nullptr, nullptr, FDL_EPILOGUE_NONE, current_stream()),
                    "matmul kernel launch failed");
     return out;
 }
@@ -145,7 +146,7 @@ Tensor linear_impl(const Tensor& input, const Tensor& weight, const Tensor& bias
     set_device(input);
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, rows, out_f, in, f32(input), in, 0,
                                 f32(weight), out_f, 0, f32(out), out_f, 0, 1, f32(bias), nullptr,
-                                epilogue, nullptr),
+                                epilogue, current_stream()),
                    "linear kernel launch failed");
     return out;
 }
@@ -187,18 +188,18 @@ LinearGrads linear_backward(const Tensor& grad_output, const Tensor& input, cons
         // dX = dY W^T  (NT)
         hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, rows, in, out_f, f32(grad_output), out_f, 0,
                                     f32(weight), out_f, 0, f32(g.grad_input), in, 0, 1, nullptr,
-                                    nullptr, FDL_EPILOGUE_NONE, nullptr),
+                                    nullptr, FDL_EPILOGUE_NONE, current_stream()),
                        "linear_backward grad_input failed");
     }
     // dW = X^T dY  (TN)
     g.grad_weight = Tensor(Shape({in, out_f}), DType::Float32, input.device());
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, in, out_f, rows, f32(input), in, 0,
                                 f32(grad_output), out_f, 0, f32(g.grad_weight), out_f, 0, 1,
-                                nullptr, nullptr, FDL_EPILOGUE_NONE, nullptr),
+                                nullptr, nullptr, FDL_EPILOGUE_NONE, current_stream()),
                    "linear_backward grad_weight failed");
     // db = column sums of dY
     g.grad_bias = Tensor(Shape({out_f}), DType::Float32, input.device());
-    hip::check_fdl(fdl_colsum(f32(grad_output), f32(g.grad_bias), rows, out_f, nullptr),
+    hip::check_fdl(fdl_colsum(f32(grad_output), f32(g.grad_bias), rows, out_f, current_stream()),
                    "linear_backward grad_bias failed");
     return g;
 }
@@ -211,7 +212,7 @@ Tensor relu(const Tensor& input) {
     check_cuda(input, "relu");
     Tensor out(input.shape(), input.dtype(), input.device());
     set_device(input);
-    hip::check_fdl(fdl_relu(f32(input), f32(out), input.numel(), nullptr),
+    hip::check_fdl(fdl_relu(f32(input), f32(out), input.numel(), current_stream()),
                    "activation kernel launch failed");
     return out;
 }
@@ -221,7 +222,7 @@ Tensor relu_backward(const Tensor& grad_output, const Tensor& activation) {
     Tensor out(grad_output.shape(), grad_output.dtype(), grad_output.device());
     set_device(grad_output);
     hip::check_fdl(fdl_relu_backward(f32(grad_output), f32(activation), f32(out),
-                                     grad_output.numel(), nullptr),
+                                     grad_output.numel(), current_stream()),
                    "relu_backward kernel launch failed");
     return out;
 }
@@ -237,7 +238,7 @@ Tensor softmax(const Tensor& input) {
     if (rows == 0 || cols == 0) throw std::runtime_error("softmax rows and cols must be non-zero");
     Tensor out(input.shape(), input.dtype(), input.device());
     set_device(input);
-    hip::check_fdl(fdl_softmax(f32(input), f32(out), rows, cols, nullptr),
+    hip::check_fdl(fdl_softmax(f32(input), f32(out), rows, cols, current_stream()),
                    "softmax kernel launch failed");
     return out;
 }
@@ -272,7 +273,7 @@ Tensor cross_entropy(const Tensor& logits, const Tensor& labels) {
     set_device(logits);
     hip::check_fdl(fdl_softmax_xent(f32(logits), static_cast<const int64_t*>(labels.data()),
                                     f32(loss), nullptr, logits.shape()[0], logits.shape()[1],
-                                    nullptr),
+                                    current_stream()),
                    "cross_entropy kernel launch failed");
     return loss;
 }
@@ -283,7 +284,7 @@ Tensor cross_entropy_backward(const Tensor& logits, const Tensor& labels) {
     set_device(logits);
     hip::check_fdl(fdl_softmax_xent(f32(logits), static_cast<const int64_t*>(labels.data()),
                                     nullptr, f32(grad), logits.shape()[0], logits.shape()[1],
-                                    nullptr),
+                                    current_stream()),
                    "cross_entropy_backward kernel launch failed");
     return grad;
 }

@@ -2,11 +2,16 @@
 // TensorImpl.cpp for the API behaviour and error strings).
 //
 // Device memory comes from a small caching allocator: freed blocks are kept
-// per (device, rounded size) and handed out again, so the ops' per-call
-// output allocation does not reach hipMalloc/hipFree in steady state.  The
-// cache is process-lifetime (never torn down at exit, when the HIP runtime
-// may already be gone).
+// per (device, rounded size, stream) and handed out again, so the ops'
+// per-call output allocation does not reach hipMalloc/hipFree in steady
+// state.  A block freed while the calling thread's current stream is S goes
+// only to later allocations made with S current: kernels still queued on S
+// that use the old tensor run before any use of the new one, by stream
+// order, while another stream would give no such order.  The cache is
+// process-lifetime (never torn down at exit, when the HIP runtime may
+// already be gone).
 #include <dl/core/HipUtils.hpp>
+#include <dl/core/Stream.hpp>
 #include <dl/kernels/random.hpp>
 #include <dl/tensor/Tensor.hpp>
 #include <dl/tensor/TensorImpl.hpp>
@@ -14,6 +19,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -42,7 +48,7 @@ public:
         const std::size_t sz = round(bytes);
         {
             std::lock_guard<std::mutex> lock(mu_);
-            auto it = free_.find({device, sz});
+            auto it = free_.find(Key{device, sz, current_stream()});
             if (it != free_.end() && !it->second.empty()) {
                 void* p = it->second.back();
                 it->second.pop_back();
@@ -61,21 +67,33 @@ public:
 
     void give_back(int device, std::size_t bytes, void* p) {
         std::lock_guard<std::mutex> lock(mu_);
-        free_[{device, round(bytes)}].push_back(p);
+        free_[Key{device, round(bytes), current_stream()}].push_back(p);
     }
 
+    // hipFree waits for the device, so blocks still used by queued work are
+    // freed only after it.
     void release_all(int device) {
         std::lock_guard<std::mutex> lock(mu_);
         for (auto& kv : free_) {
-            if (kv.first.first != device) continue;
+            if (kv.first.device != device) continue;
             for (void* p : kv.second) (void)hipFree(p);
             kv.second.clear();
         }
     }
 
 private:
+    struct Key {
+        int device;
+        std::size_t bytes;
+        void* stream;
+        bool operator<(const Key& o) const {
+            if (device != o.device) return device < o.device;
+            if (bytes != o.bytes) return bytes < o.bytes;
+            return std::less<void*>()(stream, o.stream);
+        }
+    };
     std::mutex mu_;
-    std::map<std::pair<int, std::size_t>, std::vector<void*>> free_;
+    std::map<Key, std::vector<void*>> free_;
 };
 
 const Shape& no_shape() {
@@ -138,7 +156,17 @@ void TensorImpl::copy_from_host(const void* src, std::size_t bytes) {
     if (bytes == 0) return;
     if (!device_.is_cuda()) throw std::runtime_error("copy_from_host currently supports CUDA tensors only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
-    hip::check(hipMemcpy(data_, src, bytes, hipMemcpyHostToDevice), "cudaMemcpy host to device failed");
+    // Synchronous, as the reference's cudaMemcpy: the host buffer may be
+    // reused as soon as this returns.
+    const hipStream_t s = static_cast<hipStream_t>(current_stream());
+    if (s) {
+        hip::check(hipMemcpyAsync(data_, src, bytes, hipMemcpyHostToDevice, s),
+                   "cudaMemcpy host to device failed");
+        hip::check(hipStreamSynchronize(s), "cudaMemcpy host to device failed");
+    } else {
+        hip::check(hipMemcpy(data_, src, bytes, hipMemcpyHostToDevice),
+                   "cudaMemcpy host to device failed");
+    }
 }
 
 void TensorImpl::copy_to_host(void* dst, std::size_t bytes) const {
@@ -146,7 +174,16 @@ void TensorImpl::copy_to_host(void* dst, std::size_t bytes) const {
     if (bytes == 0) return;
     if (!device_.is_cuda()) throw std::runtime_error("copy_to_host currently supports CUDA tensors only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
-    hip::check(hipMemcpy(dst, data_, bytes, hipMemcpyDeviceToHost), "cudaMemcpy device to host failed");
+    // Ordered after the work queued on the current stream, then waited for.
+    const hipStream_t s = static_cast<hipStream_t>(current_stream());
+    if (s) {
+        hip::check(hipMemcpyAsync(dst, data_, bytes, hipMemcpyDeviceToHost, s),
+                   "cudaMemcpy device to host failed");
+        hip::check(hipStreamSynchronize(s), "cudaMemcpy device to host failed");
+    } else {
+        hip::check(hipMemcpy(dst, data_, bytes, hipMemcpyDeviceToHost),
+                   "cudaMemcpy device to host failed");
+    }
 }
 
 void TensorImpl::copy_from(const TensorImpl& src) {
@@ -156,15 +193,26 @@ void TensorImpl::copy_from(const TensorImpl& src) {
         throw std::runtime_error("copy_from currently supports CUDA to CUDA only");
     }
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
-    hip::check(hipMemcpy(data_, src.data(), nbytes(), hipMemcpyDeviceToDevice),
-               "cudaMemcpy device to device failed");
+    const hipStream_t s = static_cast<hipStream_t>(current_stream());
+    if (s) {
+        hip::check(hipMemcpyAsync(data_, src.data(), nbytes(), hipMemcpyDeviceToDevice, s),
+                   "cudaMemcpy device to device failed");
+    } else {
+        hip::check(hipMemcpy(data_, src.data(), nbytes(), hipMemcpyDeviceToDevice),
+                   "cudaMemcpy device to device failed");
+    }
 }
 
 void TensorImpl::zero_() {
     if (nbytes() == 0) return;
     if (!device_.is_cuda()) throw std::runtime_error("zero_ currently supports CUDA tensors only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
-    hip::check(hipMemset(data_, 0, nbytes()), "cudaMemset failed");
+    const hipStream_t s = static_cast<hipStream_t>(current_stream());
+    if (s) {
+        hip::check(hipMemsetAsync(data_, 0, nbytes(), s), "cudaMemset failed");
+    } else {
+        hip::check(hipMemset(data_, 0, nbytes()), "cudaMemset failed");
+    }
 }
 
 // -------------------------------------------------------------------- Tensor

@@ -1,5 +1,6 @@
 // Preallocated two-layer MLP trainer over fdl_mlp2_train_step.
 #include <dl/core/HipUtils.hpp>
+#include <dl/core/Stream.hpp>
 #include <dl/train/Mlp2.hpp>
 
 #include <fastdl_gemm.h>
@@ -9,6 +10,7 @@
 #include <cmath>
 #include <limits>
 #include <stdexcept>
+#include <string>
 
 namespace dl::train {
 
@@ -42,20 +44,47 @@ Mlp2::Mlp2(int in_features, int hidden, int classes, int batch, const Device& de
     loss_ = Tensor(Shape({1}), f, device);
 }
 
-float Mlp2::step(const Tensor& x, const Tensor& labels, float lr, bool sync_loss) {
+void Mlp2::check_batch(const Tensor& x, const Tensor& labels, const char* what) const {
     if (x.shape().rank() != 2 || x.shape()[0] != batch_ || x.shape()[1] != in_ ||
         x.dtype() != DType::Float32) {
-        throw std::runtime_error("Mlp2::step: x must be float32 [batch, in_features]");
+        throw std::runtime_error(std::string(what) + ": x must be float32 [batch, in_features]");
     }
     if (labels.shape().rank() != 1 || labels.shape()[0] != batch_ || labels.dtype() != DType::Int64) {
-        throw std::runtime_error("Mlp2::step: labels must be int64 [batch]");
+        throw std::runtime_error(std::string(what) + ": labels must be int64 [batch]");
     }
+}
+
+float Mlp2::step(const Tensor& x, const Tensor& labels, float lr, bool sync_loss) {
+    check_batch(x, labels, "Mlp2::step");
     hip::check(hipSetDevice(x.device().index), "cudaSetDevice failed");
     hip::check_fdl(fdl_mlp2_train_step(fp(x), static_cast<const int64_t*>(labels.data()), batch_, in_,
                                        hidden_, classes_, fp(w1_), fp(b1_), fp(w2_), fp(b2_), lr,
                                        fp(h_), fp(logits_), fp(g2_), fp(g1_), fp(dw1_), fp(db1_),
-                                       fp(dw2_), fp(db2_), fp(dx_), fp(loss_), nullptr),
+                                       fp(dw2_), fp(db2_), fp(dx_), fp(loss_), current_stream()),
                    "Mlp2::step failed");
+    if (!sync_loss) return std::numeric_limits<float>::quiet_NaN();
+    return loss_.to_host<float>()[0];
+}
+
+void Mlp2::capture(const Tensor& x, const Tensor& labels, float lr) {
+    check_batch(x, labels, "Mlp2::capture");
+    hip::check(hipSetDevice(x.device().index), "cudaSetDevice failed");
+    fdl_mlp2_graph* g = nullptr;
+    hip::check_fdl(fdl_mlp2_graph_create(&g, fp(x), static_cast<const int64_t*>(labels.data()), batch_,
+                                         in_, hidden_, classes_, fp(w1_), fp(b1_), fp(w2_), fp(b2_),
+                                         lr, fp(h_), fp(logits_), fp(g2_), fp(g1_), fp(dw1_),
+                                         fp(db1_), fp(dw2_), fp(db2_), fp(dx_), fp(loss_),
+                                         current_stream()),
+                   "Mlp2::capture failed");
+    graph_ = std::shared_ptr<fdl_mlp2_graph>(g, [](fdl_mlp2_graph* p) { (void)fdl_mlp2_graph_destroy(p); });
+    graph_x_ = x;
+    graph_labels_ = labels;
+}
+
+float Mlp2::replay(bool sync_loss) {
+    if (!graph_) throw std::runtime_error("Mlp2::replay: no captured step");
+    hip::check(hipSetDevice(graph_x_.device().index), "cudaSetDevice failed");
+    hip::check_fdl(fdl_mlp2_graph_launch(graph_.get(), current_stream()), "Mlp2::replay failed");
     if (!sync_loss) return std::numeric_limits<float>::quiet_NaN();
     return loss_.to_host<float>()[0];
 }
@@ -70,11 +99,11 @@ Tensor Mlp2::forward(const Tensor& x) {
     hip::check(hipSetDevice(x.device().index), "cudaSetDevice failed");
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, rows, hidden_, in_, fp(x), in_, 0, fp(w1_),
                                 hidden_, 0, fp(h), hidden_, 0, 1, fp(b1_), nullptr,
-                                FDL_EPILOGUE_BIAS_RELU, nullptr),
+                                FDL_EPILOGUE_BIAS_RELU, current_stream()),
                    "Mlp2::forward failed");
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, rows, classes_, hidden_, fp(h), hidden_, 0,
                                 fp(w2_), classes_, 0, fp(out), classes_, 0, 1, fp(b2_), nullptr,
-                                FDL_EPILOGUE_BIAS, nullptr),
+                                FDL_EPILOGUE_BIAS, current_stream()),
                    "Mlp2::forward failed");
     return out;
 }

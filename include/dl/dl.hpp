@@ -4,6 +4,7 @@
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
 #include <dl/core/Shape.hpp>
+#include <dl/core/Stream.hpp>
 #include <dl/nn/Linear.hpp>
 #include <dl/nn/Module.hpp>
 #include <dl/nn/ReLU.hpp>

@@ -2,7 +2,9 @@
 // Raw-pointer GEMM launchers (reference include/dl/kernels/gemm.hpp).
 //
 // gemm() keeps the reference's signature and contract: row-major
-// C[m,n] = A[m,k] . B[k,n], C overwritten, null stream.  The GemmAlgo
+// C[m,n] = A[m,k] . B[k,n], C overwritten, enqueued on the calling thread's
+// current stream (dl/core/Stream.hpp; the null stream unless the caller
+// chose another, as in the reference).  The GemmAlgo
 // enumerators name this build's gfx950 kernel families; Auto (the default)
 // picks one by shape, as the reference's default picked cuBLAS.
 

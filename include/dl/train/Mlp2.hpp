@@ -1,13 +1,17 @@
 #pragma once
 // Native training step of the two-layer MLP  in -> hidden (ReLU) -> classes
-// with softmax cross-entropy and SGD, on preallocated device buffers (one
-// call of fdl_mlp2_train_step per step: two fused forward GEMMs, the loss
-// kernel, three backward GEMMs with the ReLU mask fused, two column sums and
-// one SGD launch; no allocation per step).
+// with softmax cross-entropy and SGD, on preallocated device buffers: one
+// call of fdl_mlp2_train_step per step (four launches for the shapes the
+// head kernel covers: layer 1 with bias+ReLU, the head with the loss and G1,
+// the grouped backward jobs, the dW1 product with both weight steps), no
+// allocation per step, on the calling thread's current stream.
 
 #include <cstdint>
+#include <memory>
 
 #include <dl/tensor/Tensor.hpp>
+
+struct fdl_mlp2_graph;  // include/fastdl_gemm.h
 
 namespace dl::train {
 
@@ -25,6 +29,16 @@ public:
     // Forward only: logits [batch, classes].
     Tensor forward(const Tensor& x);
 
+    // The step captured once into a HIP graph on the current stream and then
+    // replayed with one launch per step.  capture() records a step on x and
+    // labels with learning rate lr (refill their buffers in place between
+    // replays); nothing runs until replay().  Capturing again replaces the
+    // graph.  replay() runs one captured step on the current stream and
+    // returns the pre-update loss when sync_loss is true, else NaN; it throws
+    // if nothing was captured.
+    void capture(const Tensor& x, const Tensor& labels, float lr);
+    float replay(bool sync_loss = true);
+
     Tensor& w1() { return w1_; }
     Tensor& b1() { return b1_; }
     Tensor& w2() { return w2_; }
@@ -35,6 +49,10 @@ private:
     int in_, hidden_, classes_, batch_;
     Tensor w1_, b1_, w2_, b2_;
     Tensor h_, logits_, g2_, g1_, dw1_, db1_, dw2_, db2_, dx_, loss_;
+    std::shared_ptr<fdl_mlp2_graph> graph_;
+    Tensor graph_x_, graph_labels_;  // the captured step's inputs, kept alive
+
+    void check_batch(const Tensor& x, const Tensor& labels, const char* what) const;
 };
 
 }  // namespace dl::train

@@ -312,6 +312,70 @@ int main() {
         return ok && std::fabs(mean) < 0.1;
     });
 
+    run("stream_guard_ops_match_null_stream", [] {
+        // The same ops enqueued on a user stream give the same bits as on the
+        // null stream (every kernel is deterministic), device copies and zero
+        // fills follow the stream order, and the guard restores the stream.
+        const int m = 300, k = 200, n = 170;
+        auto a = dl::Tensor::from_host<float>(randv(m * k, 11), dl::Shape({m, k}), kDev);
+        auto b = dl::Tensor::from_host<float>(randv(k * n, 12), dl::Shape({k, n}), kDev);
+        auto bias = dl::Tensor::from_host<float>(randv(n, 13), dl::Shape({n}), kDev);
+        const auto ref_mm = dl::ops::matmul(a, b).to_host<float>();
+        const auto ref_lin = dl::ops::relu(dl::ops::linear(a, b, bias)).to_host<float>();
+        bool ok = dl::current_stream() == nullptr;
+        dl::Stream s(kDev);
+        std::vector<float> mm, lin, copied, zeroed;
+        {
+            dl::StreamGuard g(s);
+            ok = ok && dl::current_stream() == s.handle();
+            auto c = dl::ops::matmul(a, b);
+            auto y = dl::ops::relu(dl::ops::linear(a, b, bias));
+            auto c2 = dl::Tensor::empty(c.shape(), dl::DType::Float32, kDev);
+            c2.copy_from(c);
+            auto z = dl::ops::matmul(a, b);
+            z.zero_();
+            dl::synchronize();
+            mm = c.to_host<float>();
+            lin = y.to_host<float>();
+            copied = c2.to_host<float>();
+            zeroed = z.to_host<float>();
+        }
+        ok = ok && dl::current_stream() == nullptr;
+        bool zeros = true;
+        for (float v : zeroed) zeros = zeros && v == 0.0f;
+        return ok && mm == ref_mm && lin == ref_lin && copied == ref_mm && zeros;
+    });
+
+    run("mlp2_graph_replays_match_eager_steps_on_a_stream", [] {
+        const int batch = 64, in = 32, hidden = 16, classes = 10;
+        dl::train::Mlp2 eager(in, hidden, classes, batch, kDev, 5);
+        dl::train::Mlp2 graphed(in, hidden, classes, batch, kDev, 5);
+        auto x = dl::Tensor::from_host<float>(randv(batch * in, 21, 0, 1), dl::Shape({batch, in}), kDev);
+        std::vector<int64_t> lab(batch);
+        for (int i = 0; i < batch; ++i) lab[i] = (i * 3 + 1) % classes;
+        auto labels = dl::Tensor::from_host<int64_t>(lab, dl::Shape({batch}), kDev);
+        bool threw = false;
+        try {
+            graphed.replay();
+        } catch (const std::runtime_error&) {
+            threw = true;
+        }
+        dl::Stream s(kDev);
+        dl::StreamGuard g(s);
+        graphed.capture(x, labels, 0.25f);
+        bool ok = threw;
+        for (int i = 0; i < 4; ++i) {
+            const float le = eager.step(x, labels, 0.25f);
+            const float lg = graphed.replay();
+            ok = ok && std::isfinite(le) && le == lg;
+        }
+        ok = ok && eager.w1().to_host<float>() == graphed.w1().to_host<float>() &&
+             eager.b1().to_host<float>() == graphed.b1().to_host<float>() &&
+             eager.w2().to_host<float>() == graphed.w2().to_host<float>() &&
+             eager.b2().to_host<float>() == graphed.b2().to_host<float>();
+        return ok;
+    });
+
     std::cout << "api_test : " << (g_failures == 0 ? "passed" : "not passed") << std::endl;
     return g_failures == 0 ? 0 : 1;
 }

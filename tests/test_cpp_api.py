@@ -20,7 +20,7 @@ PUBLIC_HEADERS = [
     "dl/dl.hpp", "dl/core/Device.hpp", "dl/core/DType.hpp", "dl/core/Shape.hpp",
     "dl/tensor/Tensor.hpp", "dl/tensor/TensorImpl.hpp", "dl/ops/Ops.hpp", "dl/ops/OpUtils.hpp",
     "dl/nn/Module.hpp", "dl/nn/Linear.hpp", "dl/nn/ReLU.hpp", "dl/nn/Sequential.hpp",
-    "dl/kernels/kernels.hpp", "dl/optim/SGD.hpp", "dl/train/Mlp2.hpp",
+    "dl/kernels/kernels.hpp", "dl/optim/SGD.hpp", "dl/train/Mlp2.hpp", "dl/core/Stream.hpp",
 ]
 
 
@@ -46,7 +46,11 @@ def test_library_exports_api_symbols():
                 "dl::kernels::add_row_bias(float*, float const*, int, int)",
                 "dl::nn::Linear::forward(dl::Tensor const&)",
                 "dl::Tensor::kaiming_uniform(dl::Shape, dl::DType, dl::Device, unsigned long)",
-                "dl::ops::linear_backward("]:
+                "dl::ops::linear_backward(",
+                "dl::current_stream()", "dl::StreamGuard::StreamGuard(void*)",
+                "dl::Stream::Stream(dl::Device const&)",
+                "dl::train::Mlp2::capture(dl::Tensor const&, dl::Tensor const&, float)",
+                "dl::train::Mlp2::replay(bool)"]:
         assert sym in out, sym
 
 
