@@ -291,7 +291,7 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
         const int j = lane + 32 * k;
         h[k] = j < hidden ? hrow[j] : 0.0f;
     }
-    b2s[t % CM] = (t % CM) < classes ? b2[t % CM] : 0.0f;
+    if (t < CM) b2s[t] = t < classes ? b2[t] : 0.0f;
     // Sixteen loads in flight per thread before their LDS stores.
 #pragma unroll
     for (int b0 = 0; b0 < kPerThread; b0 += 16) {
