@@ -3,7 +3,7 @@
 Compiles, in-tree, with hipcc for gfx950 only:
 
 * ``fast_dl_amd/libfastdl_gemm.so`` -- HIP kernels + the C-ABI declared in
-  ``include/fastdl_gemm.h``;
+  ``include/fastdl_gemm.h`` and ``include/fastdl_data.h``;
 * ``fast_dl_amd/libfastdl.so`` -- the C++ ``dl::`` tensor/ops/nn API
   (``include/dl``) hosted on the HIP runtime, linked against the former;
 * the C++ API test programs under ``tests/cpp`` (``tests/cpp/bin``).
@@ -37,7 +37,7 @@ DEVICE_FLAGS = [
 COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-result",
                 "-I", INCLUDE, "-I", CSRC]
 
-GEMM_SOURCES = ["sgemm.hip", "mlp_kernels.hip", "capi.hip"]
+GEMM_SOURCES = ["sgemm.hip", "mlp_kernels.hip", "data_kernels.hip", "capi.hip"]
 DL_SOURCES_DIR = os.path.join(CSRC, "dl")
 
 

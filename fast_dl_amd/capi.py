@@ -31,7 +31,7 @@ _int = ctypes.c_int
 _vp = ctypes.c_void_p
 _flt = ctypes.c_float
 
-# name -> (restype, argtypes); mirrors include/fastdl_gemm.h.
+# name -> (restype, argtypes); mirrors include/fastdl_gemm.h and include/fastdl_data.h.
 SIGNATURES = {
     "fdl_sgemm_ex": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                             _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
@@ -55,6 +55,7 @@ SIGNATURES = {
     "fdl_mlp2_graph_destroy": (_int, [_vp]),
     "fdl_fill_uniform": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
     "fdl_fill_normal": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
+    "fdl_idx_gather": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _flt, _vp, _vp, _vp]),
     "fdl_last_error": (ctypes.c_char_p, []),
     "fdl_status_string": (ctypes.c_char_p, [_int]),
     "fdl_version": (ctypes.c_char_p, []),
@@ -118,6 +119,7 @@ mlp2_graph_destroy = _checked("fdl_mlp2_graph_destroy")
 
 
 fill_normal = _checked("fdl_fill_normal")
+idx_gather = _checked("fdl_idx_gather")
 
 
 def mlp2_graph_create(*args) -> int:

@@ -3,9 +3,11 @@
 // allocates memory or synchronises the stream.
 #include "fdl_internal.hpp"
 
+#include "../../include/fastdl_data.h"
 #include "../../include/fastdl_gemm.h"
 
 #include <climits>
+#include <cmath>
 #include <cstdio>
 #include <string>
 
@@ -445,6 +447,34 @@ int fdl_fill_normal(float* data, int64_t n, float mean, float stddev, uint64_t s
     if (!data) return fail(FDL_ERROR_INVALID_VALUE, "fill_normal: null pointer");
     return check_hip(fdl::launch_fill_normal(data, n, mean, stddev, seed, as_stream(stream)),
                      "fill_normal launch failed");
+}
+
+int fdl_idx_gather(const uint8_t* images, const uint8_t* labels, int64_t count,
+                   int64_t row_bytes, const int64_t* index, int64_t batch, float divisor,
+                   float* x, int64_t* y, void* stream) {
+    if (count < 0 || row_bytes < 0 || batch < 0) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: negative size");
+    }
+    if (!std::isfinite(divisor) || divisor == 0.0f) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: divisor must be finite and non-zero");
+    }
+    if (row_bytes > 0 && (count > INT64_MAX / row_bytes || batch > INT64_MAX / 4 / row_bytes)) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: sizes overflow");
+    }
+    if (batch == 0) return FDL_SUCCESS;
+    if (!x && !y) return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: x and y are both null");
+    if (x && row_bytes > 0 && count > 0 && !images) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: images is null");
+    }
+    if (y && count > 0 && !labels) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: labels is null");
+    }
+    if (!index && batch > count) {
+        return fail(FDL_ERROR_INVALID_VALUE, "idx_gather: batch exceeds count with no index");
+    }
+    return check_hip(fdl::launch_idx_gather(images, labels, count, row_bytes, index, batch,
+                                            divisor, x, y, as_stream(stream)),
+                     "idx_gather launch failed");
 }
 
 const char* fdl_last_error(void) { return g_last_error.c_str(); }

@@ -1,0 +1,160 @@
+// IDX batch gather: byte rows resident in HBM -> fp32 rows and int64 labels
+// (fdl_idx_gather in include/fastdl_data.h).
+//
+// HBM-bound streaming work: 1 byte read and 4 bytes written per pixel, plus
+// one 8-byte index per row.  Rows whose length is a multiple of 4 bytes take
+// the vector path: a chunk is 4 pixels, one dword load and one 16-byte store,
+// so a wave's loads cover 256 contiguous bytes and its stores 1 KiB.  Each
+// thread keeps kUnroll chunks in flight.  Other rows take the byte path with
+// the same structure and 1-pixel chunks.
+#include "fdl_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fdl {
+
+namespace {
+
+constexpr int kGatherThreads = 256;
+constexpr int kUnroll = 4;
+constexpr int kChunksPerBlock = kGatherThreads * kUnroll;
+
+template <int V> struct Pixels;
+template <> struct Pixels<4> { using load_t = uint32_t; using store_t = float4; };
+template <> struct Pixels<1> { using load_t = uint8_t; using store_t = float; };
+
+__device__ __forceinline__ float4 convert(uint32_t w, float divisor) {
+    return make_float4(static_cast<float>(w & 0xffu) / divisor,
+                       static_cast<float>((w >> 8) & 0xffu) / divisor,
+                       static_cast<float>((w >> 16) & 0xffu) / divisor,
+                       static_cast<float>(w >> 24) / divisor);
+}
+
+__device__ __forceinline__ float convert(uint8_t p, float divisor) {
+    return static_cast<float>(p) / divisor;
+}
+
+template <class T> __device__ __forceinline__ T zero_pixels();
+template <> __device__ __forceinline__ float4 zero_pixels<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+template <> __device__ __forceinline__ float zero_pixels<float>() { return 0.0f; }
+
+// Chunk c of the output is (row b = c / row_chunks, chunk j = c % row_chunks).
+// IdxT is uint32_t when every chunk number the grid reaches fits in it, which
+// keeps the division 32-bit.  Blocks also cover the labels: thread g < batch writes y[g].
+template <int V, class IdxT>
+__global__ void __launch_bounds__(kGatherThreads)
+idx_gather_kernel(const typename Pixels<V>::load_t* __restrict__ images,
+                  const uint8_t* __restrict__ labels, int64_t count, IdxT row_chunks,
+                  const int64_t* __restrict__ index, IdxT batch, float divisor,
+                  typename Pixels<V>::store_t* __restrict__ x, int64_t* __restrict__ y) {
+    using load_t = typename Pixels<V>::load_t;
+    using store_t = typename Pixels<V>::store_t;
+    if (x != nullptr) {
+        // total >= 1 here: x is non-null only for rows of at least one chunk.
+        // Loads are unconditional, at addresses clamped into the inputs, so
+        // that all kUnroll index loads and then all kUnroll pixel loads are in
+        // flight together; out-of-range results are discarded after the load.
+        const IdxT total = batch * row_chunks;
+        const IdxT base = static_cast<IdxT>(blockIdx.x) * kChunksPerBlock + threadIdx.x;
+        int64_t r[kUnroll];
+        IdxT j[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const IdxT c = base + static_cast<IdxT>(u) * kGatherThreads;
+            const IdxT cc = c < total ? c : total - 1;
+            const IdxT b = cc / row_chunks;
+            j[u] = cc - b * row_chunks;
+            r[u] = index != nullptr ? index[b] : static_cast<int64_t>(b);
+        }
+        load_t w[kUnroll] = {};
+        bool ok[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) ok[u] = r[u] >= 0 && r[u] < count;
+        if (count > 0) {  // count == 0 leaves no row to clamp to: nothing is loaded
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t rr = ok[u] ? r[u] : 0;
+                w[u] = images[rr * static_cast<int64_t>(row_chunks) + j[u]];
+            }
+        }
+        store_t v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = ok[u] ? convert(w[u], divisor) : zero_pixels<store_t>();
+        // Every block but the last stores without per-chunk branches, which
+        // keeps the stores back to back (a branch around each would make the
+        // next one wait for the previous store's completion count).
+        if ((static_cast<IdxT>(blockIdx.x) + 1) * kChunksPerBlock <= total) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) x[base + static_cast<IdxT>(u) * kGatherThreads] = v[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const IdxT c = base + static_cast<IdxT>(u) * kGatherThreads;
+                if (c < total) x[c] = v[u];
+            }
+        }
+    }
+    if (y != nullptr) {
+        const IdxT g = static_cast<IdxT>(blockIdx.x) * kGatherThreads + threadIdx.x;
+        if (g < batch) {
+            const int64_t r = index != nullptr ? index[g] : static_cast<int64_t>(g);
+            y[g] = (r >= 0 && r < count) ? static_cast<int64_t>(static_cast<int8_t>(labels[r])) : -1;
+        }
+    }
+}
+
+template <int V, class IdxT>
+hipError_t launch_gather(int64_t blocks, const uint8_t* images, const uint8_t* labels,
+                         int64_t count, int64_t row_bytes, const int64_t* index, int64_t batch,
+                         float divisor, float* x, int64_t* y, hipStream_t stream) {
+    using load_t = typename Pixels<V>::load_t;
+    using store_t = typename Pixels<V>::store_t;
+    hipLaunchKernelGGL((idx_gather_kernel<V, IdxT>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kGatherThreads), 0, stream, reinterpret_cast<const load_t*>(images),
+                       labels, count, static_cast<IdxT>(row_bytes / V), index,
+                       static_cast<IdxT>(batch), divisor, reinterpret_cast<store_t*>(x), y);
+    return hipGetLastError();
+}
+
+template <int V>
+hipError_t launch_gather_v(const uint8_t* images, const uint8_t* labels, int64_t count,
+                           int64_t row_bytes, const int64_t* index, int64_t batch, float divisor,
+                           float* x, int64_t* y, hipStream_t stream) {
+    const int64_t chunks = batch * (row_bytes / V);
+    const int64_t pixel_blocks = x ? (chunks + kChunksPerBlock - 1) / kChunksPerBlock : 0;
+    const int64_t label_blocks = y ? (batch + kGatherThreads - 1) / kGatherThreads : 0;
+    const int64_t blocks = pixel_blocks > label_blocks ? pixel_blocks : label_blocks;
+    if (blocks == 0) return hipSuccess;
+    if (blocks > INT32_MAX) return hipErrorInvalidConfiguration;
+    // 32-bit chunk arithmetic when every thread's largest chunk number fits.
+    if (blocks * kChunksPerBlock <= static_cast<int64_t>(UINT32_MAX)) {
+        return launch_gather<V, uint32_t>(blocks, images, labels, count, row_bytes, index, batch,
+                                          divisor, x, y, stream);
+    }
+    return launch_gather<V, uint64_t>(blocks, images, labels, count, row_bytes, index, batch,
+                                      divisor, x, y, stream);
+}
+
+}  // namespace
+
+bool idx_gather_vectorized(const uint8_t* images, int64_t row_bytes, const float* x) {
+    return row_bytes % 4 == 0 && reinterpret_cast<uintptr_t>(images) % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0;
+}
+
+hipError_t launch_idx_gather(const uint8_t* images, const uint8_t* labels, int64_t count,
+                             int64_t row_bytes, const int64_t* index, int64_t batch,
+                             float divisor, float* x, int64_t* y, hipStream_t stream) {
+    if (batch == 0) return hipSuccess;
+    if (row_bytes == 0) x = nullptr;
+    if (x == nullptr || idx_gather_vectorized(images, row_bytes, x)) {
+        return launch_gather_v<4>(images, labels, count, row_bytes, index, batch, divisor, x, y,
+                                  stream);
+    }
+    return launch_gather_v<1>(images, labels, count, row_bytes, index, batch, divisor, x, y,
+                              stream);
+}
+
+}  // namespace fdl

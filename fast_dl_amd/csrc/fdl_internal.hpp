@@ -157,4 +157,12 @@ hipError_t launch_fill_uniform(float* data, int64_t n, float low, float high,
 hipError_t launch_fill_normal(float* data, int64_t n, float mean, float stddev,
                               uint64_t seed, hipStream_t stream);
 
+// IDX batch gather (data_kernels.hip), arguments as fdl_idx_gather.  The
+// 4-pixel vector path needs row_bytes % 4 == 0, images 4-byte and x 16-byte
+// aligned; anything else takes the byte path.
+bool idx_gather_vectorized(const uint8_t* images, int64_t row_bytes, const float* x);
+hipError_t launch_idx_gather(const uint8_t* images, const uint8_t* labels, int64_t count,
+                             int64_t row_bytes, const int64_t* index, int64_t batch,
+                             float divisor, float* x, int64_t* y, hipStream_t stream);
+
 }  // namespace fdl

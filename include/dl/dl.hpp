@@ -5,6 +5,7 @@
 #include <dl/core/Device.hpp>
 #include <dl/core/Shape.hpp>
 #include <dl/core/Stream.hpp>
+#include <dl/data/DataLoader.hpp>
 #include <dl/nn/Linear.hpp>
 #include <dl/nn/Module.hpp>
 #include <dl/nn/ReLU.hpp>

@@ -53,6 +53,9 @@ _SIGS = {
                                                _vp, _vp]),
     "oracle_mlp2_grads_f64": (None, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _vp, _vp]),
+    "oracle_idx_read_images": (_int, [ctypes.c_char_p, _i64, _vp, _vp, _vp, _vp]),
+    "oracle_idx_read_labels": (_int, [ctypes.c_char_p, _i64, _vp, _vp]),
+    "oracle_idx_gather": (None, [_vp, _vp, _i64, _i64, _vp, _i64, _flt, _vp, _vp]),
 }
 
 
@@ -243,6 +246,68 @@ def mlp2_grads_f64(X, labels, W1, b1, W2, b2) -> dict:
                                 W2.shape[1], _p(W1), _p(b1), _p(W2), _p(b2), _p(g["dW1"]),
                                 _p(g["db1"]), _p(g["dW2"]), _p(g["db2"]), _p(g["dX"]))
     return g
+
+
+class IdxError(RuntimeError):
+    """An IDX file the restated loader rejects; .code is the oracle's status."""
+
+    def __init__(self, path: str, code: int):
+        super().__init__(f"{path}: IDX read failed with status {code}")
+        self.code = code
+
+
+def idx_read_images(path: str, num: int = 0) -> np.ndarray:
+    """float32 [count, rows*cols] = byte / 255 (DataLoader::load_images);
+    idx_image_dims gives count, rows and cols."""
+    count, rows, cols = (np.zeros(1, np.int64) for _ in range(3))
+    rc = lib().oracle_idx_read_images(path.encode(), num, _p(count), _p(rows), _p(cols), None)
+    if rc != 0:
+        raise IdxError(path, rc)
+    out = np.empty((int(count[0]), int(rows[0]) * int(cols[0])), np.float32)
+    rc = lib().oracle_idx_read_images(path.encode(), num, _p(count), _p(rows), _p(cols), _p(out))
+    if rc != 0:
+        raise IdxError(path, rc)
+    return out
+
+
+def idx_image_dims(path: str, num: int = 0) -> tuple[int, int, int]:
+    count, rows, cols = (np.zeros(1, np.int64) for _ in range(3))
+    rc = lib().oracle_idx_read_images(path.encode(), num, _p(count), _p(rows), _p(cols), None)
+    if rc != 0:
+        raise IdxError(path, rc)
+    return int(count[0]), int(rows[0]), int(cols[0])
+
+
+def idx_read_labels(path: str, num: int = 0) -> np.ndarray:
+    """int64 [count] labels as DataLoader::load_labels reads them."""
+    count = np.zeros(1, np.int64)
+    rc = lib().oracle_idx_read_labels(path.encode(), num, _p(count), None)
+    if rc != 0:
+        raise IdxError(path, rc)
+    out = np.empty(int(count[0]), np.int64)
+    rc = lib().oracle_idx_read_labels(path.encode(), num, _p(count), _p(out))
+    if rc != 0:
+        raise IdxError(path, rc)
+    return out
+
+
+def idx_gather(images: np.ndarray, labels: np.ndarray | None, index: np.ndarray | None,
+               batch: int | None = None, divisor: float = 255.0):
+    """(x float32 [batch, row_bytes], y int64 [batch]) as fdl_idx_gather."""
+    images = np.ascontiguousarray(images, dtype=np.uint8)
+    count, row_bytes = images.shape
+    if labels is not None:
+        labels = np.ascontiguousarray(labels, dtype=np.uint8)
+        assert labels.shape == (count,)
+    if index is not None:
+        index = np.ascontiguousarray(index, dtype=np.int64)
+        batch = index.size
+    assert batch is not None
+    x = np.empty((batch, row_bytes), np.float32)
+    y = np.empty(batch, np.int64) if labels is not None else None
+    lib().oracle_idx_gather(_p(images), _p(labels), count, row_bytes, _p(index), batch, divisor,
+                            _p(x), _p(y))
+    return x, y
 
 
 def gemm_tolerance(abs_ab: np.ndarray, K: int, c0: float = 2.0) -> np.ndarray:

@@ -8,6 +8,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -315,4 +316,94 @@ void oracle_mlp2_grads_f64(const double* X, const int64_t* labels, int64_t batch
     free(Hh);
     free(P);
     free(G1);
+}
+
+/* ------------------------------------------------------------ IDX files */
+
+/* to_int, legacy/src/data/DataLoader.cpp:22-25. */
+static int idx_word(FILE* f, int64_t* out) {
+    unsigned char p[4];
+    if (fread(p, 1, 4, f) != 4) return -3;
+    const uint32_t v = ((uint32_t)p[0] << 24) | ((uint32_t)p[1] << 16) | ((uint32_t)p[2] << 8) |
+                       (uint32_t)p[3];
+    *out = (int64_t)(int32_t)v;
+    return 0;
+}
+
+/* The num limit, DataLoader.cpp:43,85. */
+static int64_t idx_limit(int64_t count, int64_t num) {
+    return (num != 0 && num < count) ? num : count;
+}
+
+int oracle_idx_read_images(const char* path, int64_t num, int64_t* count, int64_t* rows,
+                           int64_t* cols, float* images) {
+    if (num < 0) return -4;
+    FILE* f = fopen(path, "rb");
+    if (!f) return -1;
+    int64_t magic = 0, n = 0, r = 0, c = 0;
+    int rc = idx_word(f, &magic);
+    if (rc == 0 && magic != 0x803) rc = -2;
+    if (rc == 0) rc = idx_word(f, &n);
+    if (rc == 0) rc = idx_word(f, &r);
+    if (rc == 0) rc = idx_word(f, &c);
+    if (rc == 0 && (n < 0 || r < 0 || c < 0)) rc = -4;
+    if (rc == 0) {
+        n = idx_limit(n, num);
+        *count = n;
+        *rows = r;
+        *cols = c;
+        if (images) {
+            const int64_t size = r * c;
+            unsigned char* q = (unsigned char*)malloc(size > 0 ? (size_t)size : 1);
+            for (int64_t i = 0; i < n && rc == 0; ++i) {
+                if ((int64_t)fread(q, 1, (size_t)size, f) != size) {
+                    rc = -3;
+                    break;
+                }
+                /* DataLoader.cpp:64-67 */
+                for (int64_t j = 0; j < size; ++j) images[i * size + j] = (float)q[j] / 255.0f;
+            }
+            free(q);
+        }
+    }
+    fclose(f);
+    return rc;
+}
+
+int oracle_idx_read_labels(const char* path, int64_t num, int64_t* count, int64_t* labels) {
+    if (num < 0) return -4;
+    FILE* f = fopen(path, "rb");
+    if (!f) return -1;
+    int64_t magic = 0, n = 0;
+    int rc = idx_word(f, &magic);
+    if (rc == 0 && magic != 0x801) rc = -2;
+    if (rc == 0) rc = idx_word(f, &n);
+    if (rc == 0 && n < 0) rc = -4;
+    if (rc == 0) {
+        n = idx_limit(n, num);
+        *count = n;
+        for (int64_t i = 0; labels && i < n; ++i) {
+            signed char p;
+            if (fread(&p, 1, 1, f) != 1) {
+                rc = -3;
+                break;
+            }
+            labels[i] = (int64_t)p; /* DataLoader.cpp:88-90: int label = p[0] (char) */
+        }
+    }
+    fclose(f);
+    return rc;
+}
+
+void oracle_idx_gather(const uint8_t* images, const uint8_t* labels, int64_t count,
+                       int64_t row_bytes, const int64_t* index, int64_t batch, float divisor,
+                       float* x, int64_t* y) {
+    for (int64_t b = 0; b < batch; ++b) {
+        const int64_t r = index ? index[b] : b;
+        const int ok = r >= 0 && r < count;
+        for (int64_t j = 0; x && j < row_bytes; ++j) {
+            x[b * row_bytes + j] = ok ? (float)images[r * row_bytes + j] / divisor : 0.0f;
+        }
+        if (y) y[b] = ok ? (int64_t)(int8_t)labels[r] : -1;
+    }
 }

@@ -22,6 +22,14 @@
  *   oracle_mlp2_train_step    central finite differences of the fp64 MLP
  *       loss for every parameter of a small network; the fp32 and fp64 twins
  *       agree; SGD closed form p - lr*g.
+ *   oracle_idx_read_labels    the reference's own MNIST label files (record
+ *       counts 60000 / 10000, the published per-class counts and first
+ *       labels), synthetic files with asymmetric header words (a byte-order
+ *       slip fails), a byte >= 128 read through a signed char.
+ *   oracle_idx_read_images / oracle_idx_gather  synthetic IDX3 files built
+ *       byte by byte in the tests; every byte value against the correctly
+ *       rounded quotient b/255 found from exact rationals; a gather equals
+ *       indexing the whole converted set.
  */
 #ifndef FASTDL_ORACLE_H
 #define FASTDL_ORACLE_H
@@ -121,6 +129,33 @@ void oracle_mlp2_grads_f64(const double* X, const int64_t* labels, int64_t batch
                            const double* W1, const double* b1, const double* W2,
                            const double* b2, double* dW1, double* db1, double* dW2,
                            double* db2, double* dX);
+
+/*
+ * IDX (MNIST) files, legacy/src/data/DataLoader.cpp.  Header words are
+ * big-endian 32-bit integers (to_int, :22-25).
+ *
+ * oracle_idx_read_images follows load_images (:27-72): magic 0x803, the
+ * record count cut to num when 0 < num < count (:43), rows, cols, then each
+ * pixel as (float)byte / 255.0f (:66).  With images == NULL only the header
+ * is read.  *count, *rows, *cols receive the sizes after the num limit.
+ * oracle_idx_read_labels follows load_labels (:74-93): magic 0x801, the same
+ * num limit (:85), each label byte read through a signed char (:88-89).
+ * With labels == NULL only the header is read.
+ * Both return 0, or -1 (cannot open), -2 (wrong magic), -3 (truncated file;
+ * the reference reads past the end unchecked), -4 (negative num or count).
+ */
+int oracle_idx_read_images(const char* path, int64_t num, int64_t* count, int64_t* rows,
+                           int64_t* cols, float* images);
+int oracle_idx_read_labels(const char* path, int64_t num, int64_t* count, int64_t* labels);
+
+/*
+ * The batch gather of fdl_idx_gather: r = index ? index[b] : b;
+ * x[b][j] = (float)images[r][j] / divisor and y[b] = (int8_t)labels[r] for
+ * r in [0, count), else x[b][:] = 0 and y[b] = -1.  x or y may be NULL.
+ */
+void oracle_idx_gather(const uint8_t* images, const uint8_t* labels, int64_t count,
+                       int64_t row_bytes, const int64_t* index, int64_t batch, float divisor,
+                       float* x, int64_t* y);
 
 #ifdef __cplusplus
 }

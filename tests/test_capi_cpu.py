@@ -1,6 +1,7 @@
 """CPU-side checks of the C-ABI library: it loads, exports every symbol the
 public header declares, and rejects invalid arguments before touching a GPU
 (validation never calls into the HIP runtime)."""
+import glob
 import os
 import re
 
@@ -10,21 +11,22 @@ import fast_dl_amd.capi as capi
 import oracle
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "fastdl_gemm.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(header):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(fdl_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_loads_and_exports_header_symbols():
     lib = capi.load_library()
-    names = declared_functions()
-    assert len(names) >= 15
+    assert [os.path.basename(h) for h in HEADERS] == ["fastdl_data.h", "fastdl_gemm.h"]
+    names = [n for h in HEADERS for n in declared_functions(h)]
+    assert len(names) >= 16
     for name in names:
-        assert hasattr(lib, name), f"{name} declared in fastdl_gemm.h but not exported"
+        assert hasattr(lib, name), f"{name} declared in include/*.h but not exported"
         assert name in capi.SIGNATURES, f"{name} missing from the ctypes binding"
     assert "gfx950" in capi.version()
 
@@ -128,3 +130,24 @@ def test_golden_fixtures_reproduced_by_oracle():
                                  float(m["lr"]))
     for k in ("W1", "b1", "W2", "b2", "dX", "loss"):
         assert np.array_equal(out[k], m[f"out_{k}"]), k
+
+
+def _gather_status(**kw):
+    args = dict(images=1 << 20, labels=1 << 20, count=10, row_bytes=784, index=None, batch=4,
+                divisor=255.0, x=1 << 20, y=1 << 20, stream=None)
+    args.update(kw)
+    return capi.raw_call("fdl_idx_gather", *args.values())
+
+
+def test_idx_gather_argument_validation():
+    bad = [
+        dict(count=-1), dict(row_bytes=-1), dict(batch=-1), dict(divisor=0.0),
+        dict(divisor=float("inf")), dict(divisor=float("nan")), dict(x=None, y=None),
+        dict(images=None), dict(labels=None), dict(batch=11),
+        dict(row_bytes=1 << 40, count=1 << 30),
+    ]
+    for kw in bad:
+        assert _gather_status(**kw) == -1, kw
+        assert capi.last_error().startswith("idx_gather:")
+    # no-ops and inputs that may be null: nothing is launched
+    assert _gather_status(batch=0, images=None, labels=None, x=None, y=None) == 0

@@ -21,6 +21,7 @@ PUBLIC_HEADERS = [
     "dl/tensor/Tensor.hpp", "dl/tensor/TensorImpl.hpp", "dl/ops/Ops.hpp", "dl/ops/OpUtils.hpp",
     "dl/nn/Module.hpp", "dl/nn/Linear.hpp", "dl/nn/ReLU.hpp", "dl/nn/Sequential.hpp",
     "dl/kernels/kernels.hpp", "dl/optim/SGD.hpp", "dl/train/Mlp2.hpp", "dl/core/Stream.hpp",
+    "dl/data/DataLoader.hpp",
 ]
 
 
@@ -50,7 +51,11 @@ def test_library_exports_api_symbols():
                 "dl::current_stream()", "dl::StreamGuard::StreamGuard(void*)",
                 "dl::Stream::Stream(dl::Device const&)",
                 "dl::train::Mlp2::capture(dl::Tensor const&, dl::Tensor const&, float)",
-                "dl::train::Mlp2::replay(bool)"]:
+                "dl::train::Mlp2::replay(bool)",
+                "dl::data::DataLoader::DataLoader(std::__cxx11::basic_string<",
+                "dl::data::DataLoader::gather(dl::Tensor const&, long, long, dl::Tensor&, "
+                "dl::Tensor&)",
+                "dl::data::DataLoader::getImagesMatrix(dl::Device const&)"]:
         assert sym in out, sym
 
 

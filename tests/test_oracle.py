@@ -301,3 +301,113 @@ def test_checks_catch_planted_mistakes():
     num = (ce_loss_f64(zp, lab) - ce_loss_f64(zm, lab)) / (2 * h)
     assert abs(grad[0, 1] - num) < 1e-6
     assert abs(-grad[0, 1] - num) > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# IDX files (legacy/src/data/DataLoader.cpp)
+# ---------------------------------------------------------------------------
+
+from tests import idx_files  # noqa: E402
+
+
+def test_idx_labels_match_published_mnist_facts():
+    # The reference's own label files (mnist/*-labels-idx1-ubyte, shipped as
+    # tests/golden/mnist fixtures) against published MNIST figures.
+    for path, counts, first in [
+            (idx_files.TRAIN_LABELS, idx_files.MNIST_TRAIN_CLASS_COUNTS, idx_files.MNIST_TRAIN_FIRST),
+            (idx_files.TEST_LABELS, idx_files.MNIST_TEST_CLASS_COUNTS, idx_files.MNIST_TEST_FIRST)]:
+        lab = oracle.idx_read_labels(path)
+        assert lab.size == sum(counts)
+        assert np.bincount(lab, minlength=10).tolist() == counts
+        assert lab[:10].tolist() == first
+        # the num limit keeps the first records (DataLoader.cpp:85)
+        assert oracle.idx_read_labels(path, num=7).tolist() == first[:7]
+        assert oracle.idx_read_labels(path, num=10 ** 6).size == lab.size
+
+
+def test_idx_images_synthetic_file(tmp_path):
+    g = rng(30)
+    # rows != cols and a count of 0x102 make a byte-order slip visible
+    imgs = g.integers(0, 256, (258, 3, 5), dtype=np.uint8)
+    path = str(tmp_path / "img")
+    idx_files.write_idx3(path, imgs)
+    assert oracle.idx_image_dims(path) == (258, 3, 5)
+    x = oracle.idx_read_images(path)
+    assert x.shape == (258, 15)
+    assert np.array_equal(x, imgs.reshape(258, 15).astype(np.float32) / np.float32(255))
+    assert np.array_equal(oracle.idx_read_images(path, num=4), x[:4])
+    assert oracle.idx_image_dims(path, num=300) == (258, 3, 5)
+
+
+def test_idx_pixel_conversion_is_correctly_rounded(tmp_path):
+    imgs = np.arange(256, dtype=np.uint8).reshape(1, 16, 16)
+    path = str(tmp_path / "all_bytes")
+    idx_files.write_idx3(path, imgs)
+    x = oracle.idx_read_images(path)[0]
+    assert np.array_equal(x.view(np.uint32), idx_files.correctly_rounded_quotients(255).view(np.uint32))
+    assert x[0] == 0.0 and x[255] == 1.0
+
+
+def test_idx_label_bytes_read_through_signed_char(tmp_path):
+    path = str(tmp_path / "lab")
+    idx_files.write_idx1(path, np.array([0, 9, 127, 128, 200, 255], np.uint8))
+    assert oracle.idx_read_labels(path).tolist() == [0, 9, 127, -128, -56, -1]
+
+
+def test_idx_rejects_bad_files(tmp_path):
+    imgs = np.zeros((4, 2, 2), np.uint8)
+    cases = [("magic", dict(magic=0x801), -2), ("short", dict(truncate=1), -3),
+             ("header", dict(truncate=4 * 4 + 1), -3), ("neg", dict(count=-5), -4)]
+    for name, kw, code in cases:
+        path = str(tmp_path / name)
+        idx_files.write_idx3(path, imgs, **kw)
+        with pytest.raises(oracle.IdxError) as e:
+            oracle.idx_read_images(path)
+        assert e.value.code == code, name
+    with pytest.raises(oracle.IdxError) as e:
+        oracle.idx_read_images(str(tmp_path / "missing"))
+    assert e.value.code == -1
+    path = str(tmp_path / "lab")
+    idx_files.write_idx1(path, np.arange(5, dtype=np.uint8), magic=0x803)
+    with pytest.raises(oracle.IdxError) as e:
+        oracle.idx_read_labels(path)
+    assert e.value.code == -2
+    idx_files.write_idx1(path, np.arange(5, dtype=np.uint8), truncate=1)
+    with pytest.raises(oracle.IdxError) as e:
+        oracle.idx_read_labels(path)
+    assert e.value.code == -3
+
+
+def test_idx_gather_equals_indexing():
+    g = rng(31)
+    images = g.integers(0, 256, (50, 13), dtype=np.uint8)
+    labels = g.integers(0, 256, 50, dtype=np.uint8)
+    index = np.array([3, 3, 49, 0, -1, 50, 17, 1 << 40], np.int64)
+    x, y = oracle.idx_gather(images, labels, index)
+    full = images.astype(np.float32) / np.float32(255)
+    ok = (index >= 0) & (index < 50)
+    assert np.array_equal(x[ok], full[index[ok]])
+    assert np.all(x[~ok] == 0)
+    assert np.array_equal(y[ok], labels[index[ok]].astype(np.int8).astype(np.int64))
+    assert np.all(y[~ok] == -1)
+    x2, _ = oracle.idx_gather(images, None, None, batch=50, divisor=3.0)
+    assert np.array_equal(x2, images.astype(np.float32) / np.float32(3))
+
+
+def test_idx_checks_catch_planted_mistakes(tmp_path):
+    import struct
+    raw = open(idx_files.TRAIN_LABELS, "rb").read()
+    # little-endian header words: wrong magic and count
+    magic, count = struct.unpack("<ii", raw[:8])
+    assert magic != 0x801 and count != 60000
+    # labels read as unsigned bytes: the signed-char case fails
+    assert (np.array([128, 200], np.uint8).astype(np.int64) != [-128, -56]).all()
+    # multiplying by 1/255 instead of dividing: not correctly rounded
+    b = np.arange(256, dtype=np.float32)
+    assert not np.array_equal(b * (np.float32(1) / np.float32(255)),
+                              idx_files.correctly_rounded_quotients(255))
+    # an off-by-one row in the gather fails the indexing identity
+    g = rng(32)
+    images = g.integers(0, 256, (8, 4), dtype=np.uint8)
+    x, _ = oracle.idx_gather(images, None, np.array([2, 5], np.int64))
+    assert not np.array_equal(x, images[[3, 6]].astype(np.float32) / np.float32(255))
