@@ -44,6 +44,7 @@ PROFILE_CONFIGS = {
     "c5b_1000": (1000, 1000, 1000, 0, 1, 2, 1),
     "c5b_1023": (1023, 1023, 1023, 0, 1, 2, 1),
     "c2_mlp": "mlp",
+    "idx_data": "idx",
 }
 
 
@@ -282,6 +283,81 @@ def mlp_rate(capi, torch, steps=200, warmup=20):
     return 1000.0 / ms, ms, loss, 1000.0 / gms, gms
 
 
+IDX_COUNT, IDX_PIXELS, IDX_BATCH = 60000, 784, 256  # MNIST train set: 60000 records of 28x28
+
+
+def idx_bytes(rows, pixels=IDX_PIXELS, indexed=False):
+    """Algorithmic HBM bytes of fdl_idx_gather over ``rows`` rows: 1 byte read
+    and 4 written per pixel, 1 read and 8 written per label, plus an 8-byte
+    index read per row when an index is used."""
+    return rows * (pixels * 5 + 9 + (8 if indexed else 0))
+
+
+def idx_data_rate(capi, torch, steps=30, warmup=5):
+    """fdl_idx_gather on an MNIST-sized set resident in HBM (synthetic bytes).
+    Two copies of the set and of the outputs alternate, so consecutive
+    launches touch 470 MB, more than the 256 MB Infinity Cache."""
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    count, px, B = IDX_COUNT, IDX_PIXELS, IDX_BATCH
+    copies = 2
+    imgs = [torch.randint(0, 256, (count, px), generator=gen, device="cuda",
+                          dtype=torch.uint8) for _ in range(copies)]
+    labs = [torch.randint(0, 10, (count,), generator=gen, device="cuda", dtype=torch.uint8)
+            for _ in range(copies)]
+    xs = [torch.empty((count, px), device="cuda") for _ in range(copies)]
+    ys = [torch.empty(count, device="cuda", dtype=torch.int64) for _ in range(copies)]
+    perm = torch.randperm(count, generator=gen, device="cuda")
+    xb = torch.empty((B, px), device="cuda")
+    yb = torch.empty(B, device="cuda", dtype=torch.int64)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    it = [0]
+
+    def whole(index=None):
+        i = it[0] % copies
+        it[0] += 1
+        capi.idx_gather(imgs[i].data_ptr(), labs[i].data_ptr(), count, px, index, count, 255.0,
+                        xs[i].data_ptr(), ys[i].data_ptr(), sh)
+
+    def batch():
+        j = (it[0] * B) % (count - B)
+        it[0] += 1
+        capi.idx_gather(imgs[0].data_ptr(), labs[0].data_ptr(), count, px,
+                        perm.data_ptr() + 8 * j, B, 255.0, xb.data_ptr(), yb.data_ptr(), sh)
+
+    out = {}
+    for name, fn, rows, indexed in [("whole_set", whole, count, False),
+                                    ("epoch_permuted", lambda: whole(perm.data_ptr()), count, True),
+                                    ("batch_256", batch, B, True)]:
+        warm_clock(fn, stream)
+        ms = time_launches(fn, steps, warmup, stream)
+        nbytes = idx_bytes(rows, indexed=indexed)
+        out[name] = {"ms": ms, "gbs": nbytes / (ms / 1e3) / 1e9,
+                     "frac_hbm": nbytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes}
+    return out
+
+
+def cpu_baseline_idx(seconds=2.0):
+    """The restated loader conversion (oracle_idx_gather, the loop of
+    legacy/src/data/DataLoader.cpp:61-68 over the whole set), 1 thread."""
+    import numpy as np
+
+    import oracle
+
+    g = np.random.default_rng(3)
+    images = g.integers(0, 256, (IDX_COUNT, IDX_PIXELS), dtype=np.uint8)
+    labels = g.integers(0, 10, IDX_COUNT, dtype=np.uint8)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.idx_gather(images, labels, None, batch=IDX_COUNT)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"gbs": idx_bytes(IDX_COUNT) / dt / 1e9, "ms": dt * 1e3, "cores": 1, "kind": "port",
+            "sample": f"the whole 60000x784 set, {reps} passes (oracle_idx_gather, gcc -O2)"}
+
+
 def sampled_parity(A, B, C, n, rows=16):
     """Cheap parity guard on the benchmarked output: sampled rows vs fp64 dot products."""
     import numpy as np
@@ -366,6 +442,10 @@ def sweep(capi, torch, path):
     for n in (777, 1000, 1023):
         rec(f"C5b {n}^3 bias+relu", *both(n, n, n, epi=2), 2.0 * n ** 3,
             b4(n, n, n, bias=True))
+    for name, row in idx_data_rate(capi, torch).items():
+        out.append({"config": f"IDX gather {name} (60000x784 bytes -> fp32)", "ms": row["ms"],
+                    "gbs": row["gbs"], "bound": "hbm", "frac": row["frac_hbm"]})
+        print(json.dumps(out[-1]), file=sys.stderr, flush=True)
     sps, ms, _, gsps, gms = mlp_rate(capi, torch)
     tsps, tms = torch_mlp_rate(torch)
     out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps,
@@ -394,6 +474,11 @@ def main():
     stream = torch.cuda.current_stream()
     if args.profile_mode and args.profile_config != "headline":
         cfg = PROFILE_CONFIGS[args.profile_config]
+        if cfg == "idx":
+            rows = idx_data_rate(capi, torch, steps=args.steps, warmup=args.warmup)
+            print(json.dumps({"profile_mode": True, "config": args.profile_config,
+                              "rows": rows}), flush=True)
+            return
         if cfg == "mlp" and args.profile_vendor:
             _, pms = torch_mlp_rate(torch, steps=args.steps, warmup=args.warmup)
         elif cfg == "mlp":
@@ -443,6 +528,14 @@ def main():
                "config": "784-256-10, batch 256, lr 0.1, full step (forward, softmax-CE, "
                          "backward incl. dX, SGD): one fdl_mlp2_train_step call (4 launches) "
                          "per step; graph = the same step replayed as a HIP graph"}
+    idx = None
+    if not args.no_mlp:
+        idx = idx_data_rate(capi, torch)
+        idx["workload"] = ("fdl_idx_gather over an MNIST-sized set resident in HBM: 60000 "
+                           "records of 784 bytes + label bytes -> fp32 /255 rows and int64 "
+                           "labels; batch_256 = one training batch through a permutation")
+        if not args.no_cpu:
+            idx["cpu_baseline"] = cpu_baseline_idx()
     if args.sweep:
         sweep(capi, torch, args.sweep)
 
@@ -479,6 +572,7 @@ def main():
                      "traffic": read_traffic()},
         "cpu_baseline": cpu,
         "mlp_train": mlp,
+        "idx_data": idx,
         "parity_sampled_rows_fp64": parity,
         "vendor_blas": {"what": "torch.mm fp32 (rocBLAS/hipBLASLt), same operands and stream",
                         "ms": vendor_ms, "tflops": flops / (vendor_ms / 1e3) / 1e12},

@@ -2,7 +2,9 @@
 // (fdl_idx_gather in include/fastdl_data.h).
 //
 // HBM-bound streaming work: 1 byte read and 4 bytes written per pixel, plus
-// one 8-byte index per row.  Rows whose length is a multiple of 4 bytes take
+// one 8-byte index per row.  The per-chunk integer and float work is kept to
+// a few instructions (no division per pixel or per chunk) so that the vector
+// ALU stays below the memory rate.  Rows whose length is a multiple of 4 bytes take
 // the vector path: a chunk is 4 pixels, one dword load and one 16-byte store,
 // so a wave's loads cover 256 contiguous bytes and its stores 1 KiB.  Each
 // thread keeps kUnroll chunks in flight.  Other rows take the byte path with
@@ -25,48 +27,65 @@ template <int V> struct Pixels;
 template <> struct Pixels<4> { using load_t = uint32_t; using store_t = float4; };
 template <> struct Pixels<1> { using load_t = uint8_t; using store_t = float; };
 
-__device__ __forceinline__ float4 convert(uint32_t w, float divisor) {
-    return make_float4(static_cast<float>(w & 0xffu) / divisor,
-                       static_cast<float>((w >> 8) & 0xffu) / divisor,
-                       static_cast<float>((w >> 16) & 0xffu) / divisor,
-                       static_cast<float>(w >> 24) / divisor);
+// Pixel bytes become quotients through a 256-entry table in LDS that each
+// block fills with one IEEE division per thread: the same bits as dividing
+// every pixel, at a table read per pixel instead of a division.
+static_assert(kGatherThreads == 256, "one table entry per thread");
+
+__device__ __forceinline__ float4 convert(uint32_t w, const float* lut) {
+    return make_float4(lut[w & 0xffu], lut[(w >> 8) & 0xffu], lut[(w >> 16) & 0xffu],
+                       lut[w >> 24]);
 }
 
-__device__ __forceinline__ float convert(uint8_t p, float divisor) {
-    return static_cast<float>(p) / divisor;
-}
+__device__ __forceinline__ float convert(uint8_t p, const float* lut) { return lut[p]; }
 
 template <class T> __device__ __forceinline__ T zero_pixels();
 template <> __device__ __forceinline__ float4 zero_pixels<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 template <> __device__ __forceinline__ float zero_pixels<float>() { return 0.0f; }
 
 // Chunk c of the output is (row b = c / row_chunks, chunk j = c % row_chunks).
-// IdxT is uint32_t when every chunk number the grid reaches fits in it, which
-// keeps the division 32-bit.  Blocks also cover the labels: thread g < batch writes y[g].
+// A thread's chunks are kGatherThreads apart, so after one division the next
+// (b, j) follow by adding (step_q, step_r) = divmod(kGatherThreads,
+// row_chunks) with a carry.  IdxT is uint32_t when every chunk number the
+// grid reaches fits in it.  Blocks also cover the labels: thread g < batch
+// writes y[g].
 template <int V, class IdxT>
 __global__ void __launch_bounds__(kGatherThreads)
 idx_gather_kernel(const typename Pixels<V>::load_t* __restrict__ images,
                   const uint8_t* __restrict__ labels, int64_t count, IdxT row_chunks,
-                  const int64_t* __restrict__ index, IdxT batch, float divisor,
-                  typename Pixels<V>::store_t* __restrict__ x, int64_t* __restrict__ y) {
+                  IdxT step_q, IdxT step_r, const int64_t* __restrict__ index, IdxT batch,
+                  float divisor, typename Pixels<V>::store_t* __restrict__ x,
+                  int64_t* __restrict__ y) {
     using load_t = typename Pixels<V>::load_t;
     using store_t = typename Pixels<V>::store_t;
     if (x != nullptr) {
+        __shared__ float lut[256];
+        lut[threadIdx.x] = static_cast<float>(threadIdx.x) / divisor;
+        __syncthreads();
         // total >= 1 here: x is non-null only for rows of at least one chunk.
         // Loads are unconditional, at addresses clamped into the inputs, so
         // that all kUnroll index loads and then all kUnroll pixel loads are in
         // flight together; out-of-range results are discarded after the load.
         const IdxT total = batch * row_chunks;
         const IdxT base = static_cast<IdxT>(blockIdx.x) * kChunksPerBlock + threadIdx.x;
+        const IdxT c0 = base < total ? base : total - 1;
+        IdxT b = c0 / row_chunks;
+        IdxT jj = c0 - b * row_chunks;
         int64_t r[kUnroll];
         IdxT j[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const IdxT c = base + static_cast<IdxT>(u) * kGatherThreads;
-            const IdxT cc = c < total ? c : total - 1;
-            const IdxT b = cc / row_chunks;
-            j[u] = cc - b * row_chunks;
-            r[u] = index != nullptr ? index[b] : static_cast<int64_t>(b);
+            if (u > 0) {
+                b += step_q;
+                jj += step_r;
+                if (jj >= row_chunks) {
+                    jj -= row_chunks;
+                    ++b;
+                }
+            }
+            const IdxT bc = b < batch ? b : batch - 1;  // chunks past the end: any valid row
+            j[u] = jj;
+            r[u] = index != nullptr ? index[bc] : static_cast<int64_t>(bc);
         }
         load_t w[kUnroll] = {};
         bool ok[kUnroll];
@@ -81,7 +100,7 @@ idx_gather_kernel(const typename Pixels<V>::load_t* __restrict__ images,
         }
         store_t v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = ok[u] ? convert(w[u], divisor) : zero_pixels<store_t>();
+        for (int u = 0; u < kUnroll; ++u) v[u] = ok[u] ? convert(w[u], lut) : zero_pixels<store_t>();
         // Every block but the last stores without per-chunk branches, which
         // keeps the stores back to back (a branch around each would make the
         // next one wait for the previous store's completion count).
@@ -111,10 +130,15 @@ hipError_t launch_gather(int64_t blocks, const uint8_t* images, const uint8_t* l
                          float divisor, float* x, int64_t* y, hipStream_t stream) {
     using load_t = typename Pixels<V>::load_t;
     using store_t = typename Pixels<V>::store_t;
+    const int64_t row_chunks = row_bytes / V;
+    // row_chunks may be 0 only when x is null (labels only); the steps are then unused.
+    const int64_t step_q = row_chunks > 0 ? kGatherThreads / row_chunks : 0;
+    const int64_t step_r = row_chunks > 0 ? kGatherThreads % row_chunks : 0;
     hipLaunchKernelGGL((idx_gather_kernel<V, IdxT>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kGatherThreads), 0, stream, reinterpret_cast<const load_t*>(images),
-                       labels, count, static_cast<IdxT>(row_bytes / V), index,
-                       static_cast<IdxT>(batch), divisor, reinterpret_cast<store_t*>(x), y);
+                       labels, count, static_cast<IdxT>(row_chunks), static_cast<IdxT>(step_q),
+                       static_cast<IdxT>(step_r), index, static_cast<IdxT>(batch), divisor,
+                       reinterpret_cast<store_t*>(x), y);
     return hipGetLastError();
 }
 
