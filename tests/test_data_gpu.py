@@ -5,8 +5,9 @@ Integer and byte work, so every comparison is bit-exact: against the oracle's
 restatement of legacy/src/data/DataLoader.cpp:61-68,87-90, and for the pixel
 conversion against the correctly rounded quotients found from exact
 rationals.  Cases cover the 4-pixel vector path and the byte path (odd row
-lengths, misaligned pointers), out-of-range and duplicate indices, empty
-inputs, labels-only and pixels-only calls, and the full MNIST-sized set.
+lengths, misaligned pointers), each with normal and streaming stores (outputs
+of 32 MiB and more), out-of-range and duplicate indices, empty inputs,
+labels-only and pixels-only calls, and the full MNIST-sized set.
 """
 import numpy as np
 import pytest
@@ -72,6 +73,9 @@ CASES = [
     (200, 784, 129, "perm", 255.0, 1, 0),   # misaligned images: byte path
     (200, 784, 129, "perm", 255.0, 0, 1),   # x not 16-byte aligned: byte path
     (3000, 12, 2999, None, 1.0, 0, 0),
+    # outputs of 32 MiB and more take streaming stores
+    (11000, 784, 11000, "oob", 255.0, 0, 0),
+    (12000, 785, 12000, "perm", 255.0, 0, 0),
 ]
 
 
