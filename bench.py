@@ -460,7 +460,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path's multi-GPU sharding is described in DESIGN.md", file=sys.stderr)
+              "sharding the path over several GPUs is designed, not built", file=sys.stderr)
         sys.exit(2)
     import torch
 
