@@ -2,7 +2,10 @@
 // reference (src/ops/OpUtils.cpp:20-101, Matmul.cpp:14-45, Linear.cpp:14-47,
 // Activation.cpp:13-34, Softmax.cpp:14-42, CrossEntropy.cpp:14-43); the
 // compute differs: linear's bias is fused into the GEMM epilogue instead of a
-// second pass over the output.
+// second pass over the output.  matmul, linear, linear_relu, relu and
+// cross_entropy record their backward node when an input requires a gradient.
+#include "../autograd/record.hpp"
+
 #include <dl/core/HipUtils.hpp>
 #include <dl/core/Stream.hpp>
 #include <dl/kernels/kernels.hpp>
@@ -108,6 +111,9 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
     hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, m, n, k, f32(a), k, 0, f32(b), n, 0,
                                 f32(out), n, 0, 1, nullptr, nullptr, FDL_EPILOGUE_NONE, current_stream()),
                    "matmul kernel launch failed");
+    if (autograd::any_requires_grad({&a, &b})) {
+        autograd::record(out, autograd::make_matmul_backward(a, b));
+    }
     return out;
 }
 
@@ -154,11 +160,19 @@ Tensor linear_impl(const Tensor& input, const Tensor& weight, const Tensor& bias
 }  // namespace
 
 Tensor linear(const Tensor& input, const Tensor& weight, const Tensor& bias) {
-    return linear_impl(input, weight, bias, FDL_EPILOGUE_BIAS, "linear");
+    Tensor out = linear_impl(input, weight, bias, FDL_EPILOGUE_BIAS, "linear");
+    if (autograd::any_requires_grad({&input, &weight, &bias})) {
+        autograd::record(out, autograd::make_linear_backward(input, weight, bias));
+    }
+    return out;
 }
 
 Tensor linear_relu(const Tensor& input, const Tensor& weight, const Tensor& bias) {
-    return linear_impl(input, weight, bias, FDL_EPILOGUE_BIAS_RELU, "linear_relu");
+    Tensor out = linear_impl(input, weight, bias, FDL_EPILOGUE_BIAS_RELU, "linear_relu");
+    if (autograd::any_requires_grad({&input, &weight, &bias})) {
+        autograd::record(out, autograd::make_linear_relu_backward(input, weight, bias, out));
+    }
+    return out;
 }
 
 LinearGrads linear_backward(const Tensor& grad_output, const Tensor& input, const Tensor& weight,
@@ -214,6 +228,7 @@ Tensor relu(const Tensor& input) {
     set_device(input);
     hip::check_fdl(fdl_relu(f32(input), f32(out), input.numel(), current_stream()),
                    "activation kernel launch failed");
+    if (input.requires_grad()) autograd::record(out, autograd::make_relu_backward(input));
     return out;
 }
 
@@ -275,6 +290,9 @@ Tensor cross_entropy(const Tensor& logits, const Tensor& labels) {
                                     f32(loss), nullptr, logits.shape()[0], logits.shape()[1],
                                     current_stream()),
                    "cross_entropy kernel launch failed");
+    if (logits.requires_grad()) {
+        autograd::record(loss, autograd::make_cross_entropy_backward(logits, labels));
+    }
     return loss;
 }
 

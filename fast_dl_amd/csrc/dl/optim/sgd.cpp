@@ -30,4 +30,25 @@ void SGD::step(const std::vector<Tensor*>& params, const std::vector<const Tenso
     }
 }
 
+void SGD::step(const std::vector<Tensor*>& params) const {
+    std::vector<Tensor*> ps;
+    std::vector<Tensor> gs;
+    for (Tensor* p : params) {
+        if (!p) throw std::runtime_error("SGD::step: null parameter");
+        Tensor g = p->grad();
+        if (!g.defined()) continue;
+        ps.push_back(p);
+        gs.push_back(std::move(g));
+    }
+    std::vector<const Tensor*> gp;
+    for (const Tensor& g : gs) gp.push_back(&g);
+    step(ps, gp);
+}
+
+void SGD::zero_grad(const std::vector<Tensor*>& params) {
+    for (Tensor* p : params) {
+        if (p) p->zero_grad();
+    }
+}
+
 }  // namespace dl::optim

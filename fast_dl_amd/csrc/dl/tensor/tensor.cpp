@@ -113,7 +113,9 @@ TensorImpl::TensorImpl(const Shape& shape, DType dtype, Device device)
 TensorImpl::~TensorImpl() { release(); }
 
 TensorImpl::TensorImpl(TensorImpl&& o) noexcept
-    : data_(o.data_), shape_(std::move(o.shape_)), dtype_(o.dtype_), device_(o.device_) {
+    : data_(o.data_), shape_(std::move(o.shape_)), dtype_(o.dtype_), device_(o.device_),
+      requires_grad_(o.requires_grad_), grad_(std::move(o.grad_)),
+      grad_fn_(std::move(o.grad_fn_)) {
     o.data_ = nullptr;
 }
 
@@ -124,6 +126,9 @@ TensorImpl& TensorImpl::operator=(TensorImpl&& o) noexcept {
         shape_ = std::move(o.shape_);
         dtype_ = o.dtype_;
         device_ = o.device_;
+        requires_grad_ = o.requires_grad_;
+        grad_ = std::move(o.grad_);
+        grad_fn_ = std::move(o.grad_fn_);
         o.data_ = nullptr;
     }
     return *this;

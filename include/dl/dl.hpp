@@ -1,6 +1,7 @@
 #pragma once
 // Umbrella header of the dl:: API (reference include/dl/dl.hpp).
 
+#include <dl/autograd/Node.hpp>
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
 #include <dl/core/Shape.hpp>

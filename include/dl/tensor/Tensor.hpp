@@ -16,6 +16,11 @@ namespace dl {
 
 class TensorImpl;
 
+namespace autograd {
+class Node;
+struct TensorAccess;
+}
+
 template <typename T>
 DType tensor_dtype();
 
@@ -86,7 +91,29 @@ public:
     template <typename T>
     std::vector<T> to_host() const;
 
+    // Autograd: the reference's planned interface (FUTURE_WORK.md:94-127),
+    // for the ops of the MLP path (matmul, linear, linear_relu, relu,
+    // cross_entropy).  An op records its backward node when one of its
+    // inputs requires a gradient; nothing is recorded otherwise, so code that
+    // never sets requires_grad runs as before.  Copies of a Tensor share its
+    // gradient, as they share its data.
+    bool requires_grad() const;
+    // Marks a leaf (a tensor no recorded op produced) as needing a gradient.
+    Tensor& set_requires_grad(bool requires_grad = true);
+    // The gradient accumulated into this leaf by backward() calls (float32,
+    // this tensor's shape); not defined() before the first one reaches it.
+    Tensor grad() const;
+    void zero_grad();
+    // The node that produced this tensor (null for leaves).
+    std::shared_ptr<autograd::Node> grad_fn() const;
+    // Back-propagates from this one-element float32 tensor (a loss), seeded
+    // with 1, and adds d(this)/d(leaf) to grad() of every leaf that requires
+    // a gradient.  Runs on the current stream; throws std::runtime_error if
+    // this tensor has more than one element or does not require a gradient.
+    void backward() const;
+
 private:
+    friend struct autograd::TensorAccess;  // the autograd engine's view of impl_
     std::shared_ptr<TensorImpl> impl_;
 };
 

@@ -6,12 +6,17 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
 #include <dl/core/Shape.hpp>
 
 namespace dl {
+
+namespace autograd {
+class Node;
+}
 
 class TensorImpl {
 public:
@@ -39,11 +44,24 @@ public:
     void copy_from(const TensorImpl& src);
     void zero_();
 
+    // Autograd state, as the reference plans it (FUTURE_WORK.md:100-109:
+    // grad_, requires_grad_, grad_fn_).  grad_ is the gradient accumulated by
+    // backward passes; grad_fn_ is the node that produced this tensor.
+    bool requires_grad() const { return requires_grad_; }
+    void set_requires_grad(bool v) { requires_grad_ = v; }
+    const std::shared_ptr<TensorImpl>& grad() const { return grad_; }
+    void set_grad(std::shared_ptr<TensorImpl> g) { grad_ = std::move(g); }
+    const std::shared_ptr<autograd::Node>& grad_fn() const { return grad_fn_; }
+    void set_grad_fn(std::shared_ptr<autograd::Node> fn) { grad_fn_ = std::move(fn); }
+
 private:
     void* data_ = nullptr;
     Shape shape_;
     DType dtype_ = DType::Float32;
     Device device_;
+    bool requires_grad_ = false;
+    std::shared_ptr<TensorImpl> grad_;
+    std::shared_ptr<autograd::Node> grad_fn_;
 
     void allocate();
     void release();
