@@ -337,6 +337,70 @@ def idx_data_rate(capi, torch, steps=30, warmup=5):
     return out
 
 
+def idx_epoch_rate(capi, torch, epochs=2):
+    """One training epoch of the 784-256-10 MLP (batch 256, lr 0.1) over an
+    MNIST-sized set resident in HBM, each step one fdl_mlp2_train_step.
+    "per_batch" gathers each batch (fdl_idx_gather through a permutation)
+    right before its step; "whole_epoch" gathers the epoch's 234 batches in
+    one launch into a 188 MB fp32 buffer and each step reads its rows at an
+    offset (dl::train::train_epoch's default).  steps/s over `epochs` epochs
+    after one untimed epoch."""
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    count, px, B, H, C = IDX_COUNT, IDX_PIXELS, IDX_BATCH, 256, 10
+    imgs = torch.randint(0, 256, (count, px), generator=gen, device="cuda", dtype=torch.uint8)
+    labs = torch.randint(0, C, (count,), generator=gen, device="cuda", dtype=torch.uint8)
+    perm = torch.randperm(count, generator=gen, device="cuda")
+    W1 = (torch.rand((px, H), generator=gen, device="cuda") * 2 - 1) * (6 / px) ** 0.5
+    W2 = (torch.rand((H, C), generator=gen, device="cuda") * 2 - 1) * (6 / H) ** 0.5
+    b1 = torch.zeros(H, device="cuda")
+    b2 = torch.zeros(C, device="cuda")
+    buf = {k: torch.empty(s, device="cuda") for k, s in dict(
+        H=(B, H), logits=(B, C), G2=(B, C), G1=(B, H), dW1=(px, H), db1=(H,), dW2=(H, C),
+        db2=(C,), dX=(B, px), loss=(1,)).items()}
+    p = {k: v.data_ptr() for k, v in buf.items()}
+    steps = count // B
+    xs = torch.empty((steps * B, px), device="cuda")
+    ys = torch.empty(steps * B, device="cuda", dtype=torch.int64)
+    sh = torch.cuda.current_stream().cuda_stream
+
+    def gather(row0, rows):
+        capi.idx_gather(imgs.data_ptr(), labs.data_ptr(), count, px, perm.data_ptr() + 8 * row0,
+                        rows, 255.0, xs.data_ptr(), ys.data_ptr(), sh)
+
+    def step(row0):
+        capi.mlp2_train_step(xs.data_ptr() + 4 * row0 * px, ys.data_ptr() + 8 * row0, B, px, H,
+                             C, W1.data_ptr(), b1.data_ptr(), W2.data_ptr(), b2.data_ptr(), 0.1,
+                             p["H"], p["logits"], p["G2"], p["G1"], p["dW1"], p["db1"],
+                             p["dW2"], p["db2"], p["dX"], p["loss"], sh)
+
+    def per_batch():
+        for i in range(steps):
+            gather(i * B, B)
+            step(0)
+
+    def whole_epoch():
+        gather(0, steps * B)
+        for i in range(steps):
+            step(i * B)
+
+    out = {"steps_per_epoch": steps}
+    main = torch.cuda.current_stream()
+    for name, fn in (("per_batch", per_batch), ("whole_epoch", whole_epoch)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(main)
+        for _ in range(epochs):
+            fn()
+        t1.record(main)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / epochs
+        out[name] = {"ms_per_epoch": ms, "steps_per_s": steps / (ms / 1e3)}
+    out["final_loss"] = float(buf["loss"].item())
+    return out
+
+
 def cpu_baseline_idx(seconds=2.0):
     """The restated loader conversion (oracle_idx_gather, the loop of
     legacy/src/data/DataLoader.cpp:61-68 over the whole set), 1 thread."""
@@ -446,6 +510,11 @@ def sweep(capi, torch, path):
         out.append({"config": f"IDX gather {name} (60000x784 bytes -> fp32)", "ms": row["ms"],
                     "gbs": row["gbs"], "bound": "hbm", "frac": row["frac_hbm"]})
         print(json.dumps(out[-1]), file=sys.stderr, flush=True)
+    ep = idx_epoch_rate(capi, torch)
+    out.append({"config": "MLP epoch from resident IDX bytes (234 steps of 256)",
+                "per_batch_steps_per_s": ep["per_batch"]["steps_per_s"],
+                "whole_epoch_steps_per_s": ep["whole_epoch"]["steps_per_s"]})
+    print(json.dumps(out[-1]), file=sys.stderr, flush=True)
     sps, ms, _, gsps, gms = mlp_rate(capi, torch)
     tsps, tms = torch_mlp_rate(torch)
     out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps,
@@ -531,9 +600,13 @@ def main():
     idx = None
     if not args.no_mlp:
         idx = idx_data_rate(capi, torch)
+        idx["epoch_train"] = idx_epoch_rate(capi, torch)
         idx["workload"] = ("fdl_idx_gather over an MNIST-sized set resident in HBM: 60000 "
                            "records of 784 bytes + label bytes -> fp32 /255 rows and int64 "
-                           "labels; batch_256 = one training batch through a permutation")
+                           "labels; batch_256 = one training batch through a permutation; "
+                           "epoch_train = a 784-256-10 MLP epoch (234 steps of batch 256, one "
+                           "fdl_mlp2_train_step each) fed by a gather per batch or by one "
+                           "gather of the whole epoch")
         if not args.no_cpu:
             idx["cpu_baseline"] = cpu_baseline_idx()
     if args.sweep:

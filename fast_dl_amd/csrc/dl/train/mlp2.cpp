@@ -56,8 +56,13 @@ void Mlp2::check_batch(const Tensor& x, const Tensor& labels, const char* what) 
 
 float Mlp2::step(const Tensor& x, const Tensor& labels, float lr, bool sync_loss) {
     check_batch(x, labels, "Mlp2::step");
-    hip::check(hipSetDevice(x.device().index), "cudaSetDevice failed");
-    hip::check_fdl(fdl_mlp2_train_step(fp(x), static_cast<const int64_t*>(labels.data()), batch_, in_,
+    return step(fp(x), static_cast<const int64_t*>(labels.data()), lr, sync_loss);
+}
+
+float Mlp2::step(const float* x, const int64_t* labels, float lr, bool sync_loss) {
+    if (!x || !labels) throw std::runtime_error("Mlp2::step: null batch pointer");
+    hip::check(hipSetDevice(w1_.device().index), "cudaSetDevice failed");
+    hip::check_fdl(fdl_mlp2_train_step(x, labels, batch_, in_,
                                        hidden_, classes_, fp(w1_), fp(b1_), fp(w2_), fp(b2_), lr,
                                        fp(h_), fp(logits_), fp(g2_), fp(g1_), fp(dw1_), fp(db1_),
                                        fp(dw2_), fp(db2_), fp(dx_), fp(loss_), current_stream()),

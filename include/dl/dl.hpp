@@ -14,4 +14,5 @@
 #include <dl/ops/Ops.hpp>
 #include <dl/optim/SGD.hpp>
 #include <dl/tensor/Tensor.hpp>
+#include <dl/train/Epoch.hpp>
 #include <dl/train/Mlp2.hpp>

@@ -25,6 +25,9 @@ public:
     // the pre-update loss when sync_loss is true (that reads it back, which
     // synchronises), else NaN.
     float step(const Tensor& x, const Tensor& labels, float lr, bool sync_loss = true);
+    // The same step on raw device pointers (the net's device): x holds
+    // batch * in_features floats, row-major, and labels batch int64 values.
+    float step(const float* x, const int64_t* labels, float lr, bool sync_loss = true);
 
     // Forward only: logits [batch, classes].
     Tensor forward(const Tensor& x);
@@ -44,6 +47,10 @@ public:
     Tensor& w2() { return w2_; }
     Tensor& b2() { return b2_; }
     const Tensor& grad_input() const { return dx_; }
+    // The last step's loss buffer [1] (written on the stream of that step).
+    const Tensor& loss() const { return loss_; }
+    int batch() const { return batch_; }
+    int in_features() const { return in_; }
 
 private:
     int in_, hidden_, classes_, batch_;

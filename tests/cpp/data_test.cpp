@@ -9,6 +9,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -291,6 +292,35 @@ int main() {
         }
         std::cout << "  loss " << first_loss << " -> " << last_loss << std::endl;
         return std::isfinite(last_loss) && last_loss < 0.25f * first_loss;
+    });
+
+    run("whole_epoch_gather_trains_to_the_per_batch_bits", [&] {
+        // 60000 synthetic 28x28 records with the reference's labels, batch 256:
+        // one gather for the epoch or one per step, the same arithmetic.
+        const std::string labels_path = exe_dir() + "/../../golden/mnist/train-labels-idx1-ubyte";
+        const std::string big = dir + "/epoch_images";
+        write_idx3(big, 60000, 28, 28, random_bytes(std::size_t(60000) * 784, 31));
+        dl::data::DataLoader d(big, labels_path);
+        const Tensor order = d.permutation(5, kDev);
+        dl::train::Mlp2 a(784, 256, 10, 256, kDev, 17), b(784, 256, 10, 256, kDev, 17);
+        const auto t0 = std::chrono::steady_clock::now();
+        const dl::train::EpochResult ra = dl::train::train_epoch(a, d, order, 0.05f, true);
+        const auto t1 = std::chrono::steady_clock::now();
+        const dl::train::EpochResult rb = dl::train::train_epoch(b, d, order, 0.05f, false);
+        const auto t2 = std::chrono::steady_clock::now();
+        const auto bits = [](const Tensor& p, const Tensor& q) {
+            const std::vector<float> x = p.to_host<float>(), y = q.to_host<float>();
+            return std::memcmp(x.data(), y.data(), x.size() * sizeof(float)) == 0;
+        };
+        const double ms_a = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        const double ms_b = std::chrono::duration<double, std::milli>(t2 - t1).count();
+        std::cout << "  epoch of " << ra.steps << " steps: whole-epoch gather " << ms_a
+                  << " ms, per-batch gathers " << ms_b << " ms (first epoch, includes the upload)"
+                  << std::endl;
+        std::remove(big.c_str());
+        return ra.steps == 234 && rb.steps == 234 && ra.last_loss == rb.last_loss &&
+               std::isfinite(ra.last_loss) && bits(a.w1(), b.w1()) && bits(a.b1(), b.b1()) &&
+               bits(a.w2(), b.w2()) && bits(a.b2(), b.b2());
     });
 
     // best-effort cleanup of the temporary files

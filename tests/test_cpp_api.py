@@ -21,7 +21,7 @@ PUBLIC_HEADERS = [
     "dl/tensor/Tensor.hpp", "dl/tensor/TensorImpl.hpp", "dl/ops/Ops.hpp", "dl/ops/OpUtils.hpp",
     "dl/nn/Module.hpp", "dl/nn/Linear.hpp", "dl/nn/ReLU.hpp", "dl/nn/Sequential.hpp",
     "dl/kernels/kernels.hpp", "dl/optim/SGD.hpp", "dl/train/Mlp2.hpp", "dl/core/Stream.hpp",
-    "dl/data/DataLoader.hpp", "dl/autograd/Node.hpp",
+    "dl/data/DataLoader.hpp", "dl/autograd/Node.hpp", "dl/train/Epoch.hpp",
 ]
 
 
@@ -57,6 +57,7 @@ def test_library_exports_api_symbols():
                 "dl::Tensor&)",
                 "dl::data::DataLoader::getImagesMatrix(dl::Device const&)",
                 "dl::Tensor::backward() const", "dl::Tensor::grad() const",
+                "dl::train::train_epoch(",
                 "dl::Tensor::set_requires_grad(bool)",
                 "dl::optim::SGD::step(std::vector<dl::Tensor*, std::allocator<dl::Tensor*> > const&) const"]:
         assert sym in out, sym
