@@ -1,0 +1,59 @@
+"""Seeded random sweep of fdl_mlp2_train_step against the oracle step.
+
+Shapes are drawn across the head kernel's dispatch boundaries (classes up to
+40 against the 16- and 32-class paddings, hidden up to 1100 against the 512
+and 1024 limits, batches that are not multiples of its 8 rows, dW1 too small
+for its records) so both the four-launch and the six-launch step are reached,
+with and without dX, and some labels outside [0, classes) (left out of the
+loss, as the reference's cross_entropy does).  Bar: every intermediate and
+updated parameter within 2e-5 normwise of the fp32 oracle step, loss within
+1e-5.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_helpers import say
+from tests.test_mlp_gpu import _step_gpu
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 120
+
+
+def _draw(g):
+    B = int(g.choice([1, 2, 7, 8, 9, 31, 64, 100, 255, 256, 300]))
+    I = int(np.exp(g.uniform(0, np.log(800))))
+    H = int(g.choice([1, 3, 16, 100, 255, 256, 257, 511, 512, 513, 700, 1024, 1025, 1100]))
+    C = int(g.choice([1, 2, 9, 10, 15, 16, 17, 31, 32, 33, 40]))
+    with_dx = bool(g.integers(0, 4) > 0)
+    invalid = bool(g.integers(0, 4) == 0)
+    return B, I, H, C, with_dx, invalid
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_random_mlp_step(device, case):
+    g = np.random.default_rng(2000 + case)
+    B, I, H, C, with_dx, invalid = _draw(g)
+    X = g.random((B, I)).astype(np.float32)
+    labels = g.integers(0, C, B).astype(np.int64)
+    if invalid:
+        labels[::5] = -1
+        labels[2::7] = C
+    W1 = g.uniform(-np.sqrt(6 / I), np.sqrt(6 / I), (I, H)).astype(np.float32)
+    W2 = g.uniform(-np.sqrt(6 / H), np.sqrt(6 / H), (H, C)).astype(np.float32)
+    b1 = (g.standard_normal(H) * 0.1).astype(np.float32)
+    b2 = (g.standard_normal(C) * 0.1).astype(np.float32)
+    say(f"random mlp2 step case {case}: B={B} I={I} H={H} C={C} dx={with_dx} invalid={invalid}")
+    gpu = _step_gpu(X, labels, W1, b1, W2, b2, 0.05, with_dx=with_dx)
+    ref = oracle.mlp2_train_step(X, labels, W1, b1, W2, b2, 0.05, with_dx=with_dx)
+    names = ["H", "logits", "G2", "G1", "dW1", "db1", "dW2", "db2", "W1", "b1", "W2", "b2"]
+    if with_dx:
+        names.append("dX")
+    for name in names:
+        a = gpu[name].astype(np.float64)
+        b = ref[name].astype(np.float64)
+        assert np.all(np.isfinite(a)), name
+        err = np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b)))
+        assert err <= 2e-5, f"{name}: normwise error {err:.2e}"
+    assert abs(gpu["loss"][0] - ref["loss"][0]) <= 1e-5
