@@ -110,6 +110,26 @@ int main() {
         return ok && a.grad().shape().dims == a.shape().dims && !c.grad().defined();
     });
 
+    run("a_tensor_used_twice_gets_both_contributions", [] {
+        // C = A A: dA = dC A^T + A^T dC, accumulated from the node's two inputs.
+        const int m = 23, classes = m;
+        Tensor a = Tensor::from_host(randv(m * m, 31), Shape({m, m}), kDev);
+        a.set_requires_grad();
+        const Tensor labels = Tensor::from_host(labels_of(m, classes, 32), Shape({m}), kDev);
+        const Tensor c = dl::ops::matmul(a, a);
+        dl::ops::cross_entropy(c, labels).backward();
+        const std::vector<float> dc = dl::ops::cross_entropy_backward(c, labels).to_host<float>();
+        const std::vector<float> ah = a.to_host<float>();
+        std::vector<double> da(m * m, 0.0);
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < m; ++j)
+                for (int k = 0; k < m; ++k) {
+                    da[i * m + k] += double(dc[i * m + j]) * ah[k * m + j];  // dC A^T
+                    da[k * m + j] += double(ah[i * m + k]) * dc[i * m + j];  // A^T dC
+                }
+        return close(a.grad().to_host<float>(), da, 1e-5);
+    });
+
     run("mlp_gradients_equal_the_explicit_backward_ops", [] {
         const int batch = 64, in = 96, hidden = 48, classes = 10;
         dl::nn::Sequential model;
