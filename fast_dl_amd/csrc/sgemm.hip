@@ -1876,16 +1876,21 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     if (p.M <= 8 && !transB && p.N >= 64) return GemmKernel::Skinny;
     const int64_t t64 = (int64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
     constexpr int64_t kCUs = 256;
-    // Too few 64x64 tiles to occupy the GPU, or too short a K loop to
-    // amortise LDS staging: split K over the waves of a block instead, with
-    // 16x16 output tiles when 32x32 ones would leave most CUs idle.  Short K
-    // needs a full GPU of 64x64 tiles and ~128 tiles of 128x128 (the C4 batch
-    // of 64 128x128x64 problems: split-K 5.8 vs 6.8 us for a tile kernel);
-    // with K >= 256 the 64x64 direct-to-LDS tile wins from ~160 tiles
-    // (777^3: 21.9 vs 25.2 us; 1024^3: 22 vs 42 us).
+    // Too few 64x64 tiles to occupy the GPU: split K over the waves of a
+    // block instead, with 16x16 output tiles when 32x32 ones would leave most
+    // CUs idle.  With K >= 256 the 64x64 direct-to-LDS tile wins from ~160
+    // tiles (777^3: 21.9 vs 25.2 us; 1024^3: 22 vs 42 us).  Short K (64 to
+    // 255) needs a full GPU of 64x64 tiles (the C4 batch of 64 128x128x64
+    // problems: 5.0-5.2 vs 6.1-6.2 us for split-K; 1024x1024x128: 6.5 vs 8.4
+    // us).  Below 128 tiles of 128x128, split-K still wins when the 64x64
+    // tile count passes a multiple of the CU count by only a few tiles, whose
+    // second round would run nearly empty (1000x1100x96 NT, 288 tiles:
+    // split-K 8.7 vs 9.1 us).
     const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+    const int64_t rem = t64 % kCUs;
     const bool long_k = p.K >= 256;
-    if (p.K < 64 || t64 < (long_k ? 160 : kCUs) || (t128 < 128 && !long_k)) {
+    if (p.K < 64 || t64 < (long_k ? 160 : kCUs) ||
+        (!long_k && t128 < 128 && rem > 0 && rem < 64)) {
         const int64_t t32 = (int64_t)((p.M + 31) / 32) * ((p.N + 31) / 32) * batch;
         return t32 < 128 ? GemmKernel::SplitK16 : GemmKernel::SplitK32;
     }

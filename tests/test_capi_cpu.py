@@ -96,8 +96,12 @@ def test_kernel_choice():
     assert capi.kernel_choice(0, 0, 1000, 1000, 1000) == capi.KERNEL_DMA64
     assert capi.kernel_choice(0, 0, 1023, 1023, 1023) == capi.KERNEL_DMA64U
     assert capi.kernel_choice(0, 0, 777, 777, 777) == capi.KERNEL_DMA64U
-    # a short K stays on split-K (the C4 batch)
-    assert capi.kernel_choice(0, 0, 128, 128, 64, 64) == capi.KERNEL_SPLITK32
+    # short K: a full GPU of 64x64 tiles takes the 64x64 tile (the C4 batch),
+    # a tile count just past one round stays on split-K
+    assert capi.kernel_choice(0, 0, 128, 128, 64, 64) == capi.KERNEL_DMA64
+    assert capi.kernel_choice(0, 1, 128, 128, 64, 64) == capi.KERNEL_DMA64
+    assert capi.kernel_choice(0, 1, 1000, 1100, 96) == capi.KERNEL_SPLITK32
+    assert capi.kernel_choice(0, 0, 1024, 1024, 32) == capi.KERNEL_SPLITK32
     # about one 128x128 tile per CU: the eight-wave 128x128 tile; three per CU:
     # the two-blocks-per-CU 128x128 tile
     assert capi.kernel_choice(0, 0, 2048, 2048, 2048) == capi.KERNEL_DMA128W8
