@@ -2,13 +2,14 @@
 // (fdl_idx_gather in include/fastdl_data.h).
 //
 // HBM-bound streaming work: 1 byte read and 4 bytes written per pixel, plus
-// one 8-byte index per row.  The per-chunk integer and float work is kept to
-// a few instructions (no division per pixel or per chunk) so that the vector
-// ALU stays below the memory rate.  Rows whose length is a multiple of 4 bytes take
-// the vector path: a chunk is 4 pixels, one dword load and one 16-byte store,
-// so a wave's loads cover 256 contiguous bytes and its stores 1 KiB.  Each
-// thread keeps kUnroll chunks in flight.  Other rows take the byte path with
-// the same structure and 1-pixel chunks.
+// one 8-byte index per row.  The per-chunk work is a few instructions (a
+// quotient-table read per pixel, one integer division per thread) so that the
+// vector ALU stays below the memory rate.  Rows whose length is a multiple of
+// 4 bytes take the vector path: a chunk is 4 pixels, one dword load and one
+// 16-byte store, so a wave's loads cover 256 contiguous bytes and its stores
+// 1 KiB.  Each thread keeps kUnroll chunks in flight.  Other rows take the
+// byte path with the same structure and 1-pixel chunks.  Outputs of 32 MiB
+// and more are written with streaming stores.
 #include "fdl_internal.hpp"
 
 #include <hip/hip_runtime.h>
