@@ -8,6 +8,8 @@
 
 #include <fastdl_gemm.h>
 
+#include "../tensor/block_cache.hpp"
+
 #include <hip/hip_runtime_api.h>
 
 #include <sstream>
@@ -84,21 +86,39 @@ Stream::Stream(const Device& device) {
     hipStream_t s = nullptr;
     hip::check(hipStreamCreate(&s), "stream create failed");
     stream_ = s;
+    detail::device_block_cache().stream_created(stream_);
 }
 
-Stream::~Stream() {
-    if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+namespace {
+
+// Hands the stream's cached blocks to the shared pool (after its work has
+// finished), then destroys it.
+void destroy_stream(void* stream) noexcept {
+    if (!stream) return;
+    try {
+        detail::device_block_cache().retire_stream(stream);
+    } catch (...) {
+        // The stream could not be synchronized; its blocks stay filed under
+        // its handle and are freed on the next out-of-memory retry.
+    }
+    (void)hipStreamDestroy(static_cast<hipStream_t>(stream));
 }
+
+}  // namespace
+
+Stream::~Stream() { destroy_stream(stream_); }
 
 Stream::Stream(Stream&& other) noexcept : stream_(std::exchange(other.stream_, nullptr)) {}
 
 Stream& Stream::operator=(Stream&& other) noexcept {
     if (this != &other) {
-        if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+        destroy_stream(stream_);
         stream_ = std::exchange(other.stream_, nullptr);
     }
     return *this;
 }
+
+void retire_stream(void* stream) { detail::device_block_cache().retire_stream(stream); }
 
 void Stream::synchronize() const {
     hip::check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "stream synchronize failed");

@@ -1,15 +1,16 @@
 // Tensor / TensorImpl on the HIP runtime (reference src/tensor/Tensor.cpp and
 // TensorImpl.cpp for the API behaviour and error strings).
 //
-// Device memory comes from a small caching allocator: freed blocks are kept
-// per (device, rounded size, stream) and handed out again, so the ops'
-// per-call output allocation does not reach hipMalloc/hipFree in steady
-// state.  A block freed while the calling thread's current stream is S goes
-// only to later allocations made with S current: kernels still queued on S
-// that use the old tensor run before any use of the new one, by stream
-// order, while another stream would give no such order.  The cache is
-// process-lifetime (never torn down at exit, when the HIP runtime may
-// already be gone).
+// Device memory comes from the stream-ordered block cache of
+// block_cache.hpp: a tensor's block belongs to the stream that was current
+// when it was allocated and goes back to that stream's free list when the
+// tensor dies; streams other than that one which the tensor's memory was
+// used on (every data() call records the calling thread's current stream)
+// hold the block back until they pass an event recorded at the release.  The
+// cache is process-lifetime (never torn down at exit, when the HIP runtime
+// may already be gone).
+#include "block_cache.hpp"
+
 #include <dl/core/HipUtils.hpp>
 #include <dl/core/Stream.hpp>
 #include <dl/kernels/random.hpp>
@@ -18,83 +19,135 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cmath>
-#include <functional>
-#include <map>
 #include <mutex>
 #include <stdexcept>
+#include <string>
 #include <utility>
 #include <vector>
 
 namespace dl {
 
+namespace detail {
+
 namespace {
 
-class BlockCache {
+std::atomic<int> g_inject_failures{0};
+
+// The cache's view of the HIP runtime.  A failed call that the cache
+// recovers from (an allocation it retries, an event not yet reached) must
+// not leave HIP's per-thread error state set: every launcher in this library
+// reports hipGetLastError() after its launch, so a stale failure would be
+// reported by the next, unrelated op.  The state is cleared only when it was
+// clear before the call, so an earlier failure is still reported.
+class HipBackend final : public CacheBackend {
 public:
-    static BlockCache& get() {
-        static BlockCache* cache = new BlockCache();
-        return *cache;
-    }
-
-    static std::size_t round(std::size_t bytes) {
-        constexpr std::size_t kSmall = 512;
-        constexpr std::size_t kLarge = std::size_t(2) << 20;
-        const std::size_t g = bytes < kLarge ? kSmall : kLarge;
-        return (bytes + g - 1) / g * g;
-    }
-
-    void* acquire(int device, std::size_t bytes) {
-        const std::size_t sz = round(bytes);
+    bool alloc(int device, std::size_t bytes, void** p) override {
+        hip::check(hipSetDevice(device), "cudaSetDevice failed");
+        const hipError_t before = hipPeekAtLastError();
+        std::size_t ask = bytes;
+        int left = g_inject_failures.load();
+        while (left > 0 && !g_inject_failures.compare_exchange_weak(left, left - 1)) {
+        }
+        if (left > 0) ask = std::size_t(1) << 62;  // more than any device holds
+        *p = nullptr;
+        hipError_t err = hipMalloc(p, ask);
+        if (err == hipSuccess && ask != bytes) {
+            (void)hipFree(*p);
+            *p = nullptr;
+            err = hipErrorOutOfMemory;
+        }
+        if (err == hipSuccess) return true;
         {
             std::lock_guard<std::mutex> lock(mu_);
-            auto it = free_.find(Key{device, sz, current_stream()});
-            if (it != free_.end() && !it->second.empty()) {
-                void* p = it->second.back();
-                it->second.pop_back();
-                return p;
+            last_ = hipGetErrorString(err);
+        }
+        *p = nullptr;
+        if (before == hipSuccess) (void)hipGetLastError();
+        return false;
+    }
+
+    void free(int device, void* p) override {
+        (void)hipSetDevice(device);
+        (void)hipFree(p);
+    }
+
+    // Runs in tensor destructors, so it does not throw: if no event can be
+    // recorded it waits for the stream instead and returns no marker (done).
+    void* mark(int device, void* stream) override {
+        hipEvent_t ev = nullptr;
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            if (!pool_.empty()) {
+                ev = pool_.back();
+                pool_.pop_back();
             }
         }
-        void* p = nullptr;
-        hipError_t err = hipMalloc(&p, sz);
-        if (err != hipSuccess) {
-            // Return every cached block of this device to HIP and retry once.
-            release_all(device);
-            hip::check(hipMalloc(&p, sz), "cudaMalloc failed");
-        }
-        return p;
+        const hipError_t before = hipPeekAtLastError();
+        hipError_t err = hipSetDevice(device);
+        if (err == hipSuccess && !ev) err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (err == hipSuccess) err = hipEventRecord(ev, static_cast<hipStream_t>(stream));
+        if (err == hipSuccess) return ev;
+        if (ev) drop(ev);
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
+        if (before == hipSuccess) (void)hipGetLastError();
+        return nullptr;
     }
 
-    void give_back(int device, std::size_t bytes, void* p) {
-        std::lock_guard<std::mutex> lock(mu_);
-        free_[Key{device, round(bytes), current_stream()}].push_back(p);
+    bool done(void* marker) override {
+        if (!marker) return true;
+        const hipError_t before = hipPeekAtLastError();
+        const hipError_t q = hipEventQuery(static_cast<hipEvent_t>(marker));
+        if (q == hipSuccess) return true;
+        if (before == hipSuccess) (void)hipGetLastError();
+        if (q == hipErrorNotReady) return false;
+        hip::check(q, "event query failed");
+        return false;
     }
 
-    // hipFree waits for the device, so blocks still used by queued work are
-    // freed only after it.
-    void release_all(int device) {
+    void wait(void* marker) override {
+        if (!marker) return;
+        hip::check(hipEventSynchronize(static_cast<hipEvent_t>(marker)),
+                   "event synchronize failed");
+    }
+
+    void drop(void* marker) override {
+        if (!marker) return;
         std::lock_guard<std::mutex> lock(mu_);
-        for (auto& kv : free_) {
-            if (kv.first.device != device) continue;
-            for (void* p : kv.second) (void)hipFree(p);
-            kv.second.clear();
-        }
+        pool_.push_back(static_cast<hipEvent_t>(marker));
+    }
+
+    void sync(void* stream) override {
+        hip::check(hipStreamSynchronize(static_cast<hipStream_t>(stream)),
+                   "stream synchronize failed");
+    }
+
+    std::string last_error() override {
+        std::lock_guard<std::mutex> lock(mu_);
+        return last_;
     }
 
 private:
-    struct Key {
-        int device;
-        std::size_t bytes;
-        void* stream;
-        bool operator<(const Key& o) const {
-            if (device != o.device) return device < o.device;
-            if (bytes != o.bytes) return bytes < o.bytes;
-            return std::less<void*>()(stream, o.stream);
-        }
-    };
     std::mutex mu_;
-    std::map<Key, std::vector<void*>> free_;
+    std::string last_;
+    std::vector<hipEvent_t> pool_;
 };
+
+}  // namespace
+
+BlockCache& device_block_cache() {
+    static HipBackend* backend = new HipBackend();
+    static BlockCache* cache = new BlockCache(*backend);
+    return *cache;
+}
+
+void inject_alloc_failures(int n) { g_inject_failures.store(std::max(0, n)); }
+
+}  // namespace detail
+
+namespace {
 
 const Shape& no_shape() {
     static const Shape s;
@@ -113,7 +166,8 @@ TensorImpl::TensorImpl(const Shape& shape, DType dtype, Device device)
 TensorImpl::~TensorImpl() { release(); }
 
 TensorImpl::TensorImpl(TensorImpl&& o) noexcept
-    : data_(o.data_), shape_(std::move(o.shape_)), dtype_(o.dtype_), device_(o.device_),
+    : data_(o.data_), stream_(o.stream_), uses_(std::move(o.uses_)),
+      shape_(std::move(o.shape_)), dtype_(o.dtype_), device_(o.device_),
       requires_grad_(o.requires_grad_), grad_(std::move(o.grad_)),
       grad_fn_(std::move(o.grad_fn_)) {
     o.data_ = nullptr;
@@ -123,6 +177,8 @@ TensorImpl& TensorImpl::operator=(TensorImpl&& o) noexcept {
     if (this != &o) {
         release();
         data_ = o.data_;
+        stream_ = o.stream_;
+        uses_ = std::move(o.uses_);
         shape_ = std::move(o.shape_);
         dtype_ = o.dtype_;
         device_ = o.device_;
@@ -134,8 +190,24 @@ TensorImpl& TensorImpl::operator=(TensorImpl&& o) noexcept {
     return *this;
 }
 
-void* TensorImpl::data() { return data_; }
-const void* TensorImpl::data() const { return data_; }
+void* TensorImpl::data() {
+    note_use();
+    return data_;
+}
+
+const void* TensorImpl::data() const {
+    note_use();
+    return data_;
+}
+
+void TensorImpl::note_use() const {
+    if (data_) record_stream(current_stream());
+}
+
+void TensorImpl::record_stream(void* stream) const {
+    if (stream == stream_ || std::find(uses_.begin(), uses_.end(), stream) != uses_.end()) return;
+    uses_.push_back(stream);
+}
 const Shape& TensorImpl::shape() const { return shape_; }
 DType TensorImpl::dtype() const { return dtype_; }
 Device TensorImpl::device() const { return device_; }
@@ -147,13 +219,17 @@ void TensorImpl::allocate() {
     if (bytes == 0) return;
     if (!device_.is_cuda()) throw std::runtime_error("Tensor currently supports CUDA allocation only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
-    data_ = BlockCache::get().acquire(device_.index, bytes);
+    stream_ = current_stream();
+    data_ = detail::device_block_cache().acquire(device_.index, bytes, stream_);
 }
 
 void TensorImpl::release() {
     if (!data_) return;
-    if (device_.is_cuda()) BlockCache::get().give_back(device_.index, nbytes(), data_);
+    if (device_.is_cuda()) {
+        detail::device_block_cache().release(device_.index, nbytes(), data_, stream_, uses_);
+    }
     data_ = nullptr;
+    uses_.clear();
 }
 
 void TensorImpl::copy_from_host(const void* src, std::size_t bytes) {
@@ -198,6 +274,8 @@ void TensorImpl::copy_from(const TensorImpl& src) {
         throw std::runtime_error("copy_from currently supports CUDA to CUDA only");
     }
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
+    note_use();
+    src.note_use();
     const hipStream_t s = static_cast<hipStream_t>(current_stream());
     if (s) {
         hip::check(hipMemcpyAsync(data_, src.data(), nbytes(), hipMemcpyDeviceToDevice, s),
@@ -212,6 +290,7 @@ void TensorImpl::zero_() {
     if (nbytes() == 0) return;
     if (!device_.is_cuda()) throw std::runtime_error("zero_ currently supports CUDA tensors only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
+    note_use();
     const hipStream_t s = static_cast<hipStream_t>(current_stream());
     if (s) {
         hip::check(hipMemsetAsync(data_, 0, nbytes(), s), "cudaMemset failed");
@@ -314,6 +393,10 @@ void Tensor::copy_from(const Tensor& src) {
 }
 
 void Tensor::copy_to(Tensor& dst) const { dst.copy_from(*this); }
+
+void Tensor::record_stream(void* stream) const {
+    if (impl_ && impl_->data_ptr_raw()) impl_->record_stream(stream);
+}
 
 void Tensor::zero_() {
     if (!impl_) throw std::runtime_error("zero_ requires a defined tensor");

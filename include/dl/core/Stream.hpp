@@ -30,8 +30,16 @@ private:
 // The stream every dl:: op, kernel launcher, tensor transfer and trainer step
 // issued from the calling thread is enqueued on; nullptr (the default) is the
 // null stream.  Tensor transfers to and from the host stay synchronous.
+//
+// Tensor memory is cached per stream: a tensor's block returns to the stream
+// that was current when it was allocated.  A dl::Stream hands its cached
+// blocks back when it is destroyed.  A raw hipStream_t made current with
+// set_current_stream must be passed to retire_stream before the caller
+// destroys it (that waits for its work and releases its cached blocks to
+// every stream).
 void* current_stream();
 void set_current_stream(void* stream);
+void retire_stream(void* stream);
 
 // Makes `stream` the calling thread's current stream for the guard's lifetime
 // and restores the previous one on destruction.

@@ -87,6 +87,12 @@ public:
     void copy_from(const Tensor& src);
     void copy_to(Tensor& dst) const;
     void zero_();
+    // Marks the memory as used by work on `stream` (a hipStream_t), so that
+    // it is not reused before that work when this tensor dies.  data() and
+    // every dl:: op record the calling thread's current stream by
+    // themselves; this is for work queued on another stream through a raw
+    // pointer.
+    void record_stream(void* stream) const;
 
     template <typename T>
     std::vector<T> to_host() const;

@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <vector>
 
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
@@ -29,8 +30,12 @@ public:
     TensorImpl(TensorImpl&& other) noexcept;
     TensorImpl& operator=(TensorImpl&& other) noexcept;
 
+    // The device pointer.  Also records the calling thread's current stream
+    // as a stream this memory is used on (see record_stream).
     void* data();
     const void* data() const;
+    // The pointer without recording a use.
+    const void* data_ptr_raw() const { return data_; }
 
     const Shape& shape() const;
     DType dtype() const;
@@ -54,8 +59,19 @@ public:
     const std::shared_ptr<autograd::Node>& grad_fn() const { return grad_fn_; }
     void set_grad_fn(std::shared_ptr<autograd::Node> fn) { grad_fn_ = std::move(fn); }
 
+    // The stream that was current when the memory was allocated: the block
+    // returns to that stream's free list when this tensor dies, whichever
+    // stream is current then.
+    void* stream() const { return stream_; }
+    // Records that the memory is used by work on `stream`.  When the tensor
+    // dies, the block is not handed out again until every such stream other
+    // than stream() has passed that point.
+    void record_stream(void* stream) const;
+
 private:
     void* data_ = nullptr;
+    void* stream_ = nullptr;
+    mutable std::vector<void*> uses_;
     Shape shape_;
     DType dtype_ = DType::Float32;
     Device device_;
@@ -65,6 +81,7 @@ private:
 
     void allocate();
     void release();
+    void note_use() const;
 };
 
 }  // namespace dl

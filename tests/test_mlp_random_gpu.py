@@ -36,8 +36,9 @@ def _draw(g):
     return B, I, H, C, with_dx, invalid
 
 
-@pytest.mark.parametrize("case", range(N_CASES))
-def test_random_mlp_step(device, case):
+def case_inputs(case):
+    """Inputs of sweep case `case` (seeded by the case number):
+    (X, labels, W1, b1, W2, b2, with_dx, invalid)."""
     g = np.random.default_rng(2000 + case)
     B, I, H, C, with_dx, invalid = _draw(g)
     X = g.random((B, I)).astype(np.float32)
@@ -49,6 +50,13 @@ def test_random_mlp_step(device, case):
     W2 = g.uniform(-np.sqrt(6 / H), np.sqrt(6 / H), (H, C)).astype(np.float32)
     b1 = (g.standard_normal(H) * 0.1).astype(np.float32)
     b2 = (g.standard_normal(C) * 0.1).astype(np.float32)
+    return X, labels, W1, b1, W2, b2, with_dx, invalid
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_random_mlp_step(device, case):
+    X, labels, W1, b1, W2, b2, with_dx, invalid = case_inputs(case)
+    (B, I), H, C = X.shape, W1.shape[1], W2.shape[1]
     say(f"random mlp2 step case {case}: B={B} I={I} H={H} C={C} dx={with_dx} invalid={invalid}")
     gpu = _step_gpu(X, labels, W1, b1, W2, b2, 0.05, with_dx=with_dx)
     ref = oracle.mlp2_train_step(X, labels, W1, b1, W2, b2, 0.05, with_dx=with_dx)
