@@ -28,24 +28,15 @@ PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix peak (256 CU x 256 FLO
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sgemm_nn_4096_traffic.txt")
 
-# --profile-mode workloads: name -> (M, N, K, transB, batch, epilogue, rotate).
+# --profile-mode workloads (fast_dl_amd/profiling.py): name -> (M, N, K, transB,
+# batch, epilogue, rotate), or "mlp" / "idx" for the MLP step and the IDX gather.
 # "headline" is the bench line's own GEMM (M = N = K = --size).
-PROFILE_CONFIGS = {
-    "headline": None,
-    "c1": (256, 128, 784, 0, 1, 0, 1),
-    "c3_1024": (1024, 1024, 1024, 0, 1, 0, 1),
-    "c3_2048": (2048, 2048, 2048, 0, 1, 0, 1),
-    "c3_8192": (8192, 8192, 8192, 0, 1, 0, 1),
-    "c4_nn": (128, 128, 64, 0, 64, 0, 40),
-    "c4_nt": (128, 128, 64, 1, 64, 0, 40),
-    "c5a_m1": (1, 4096, 4096, 0, 1, 2, 6),
-    "c5a_m8": (8, 4096, 4096, 0, 1, 2, 6),
-    "c5b_777": (777, 777, 777, 0, 1, 2, 1),
-    "c5b_1000": (1000, 1000, 1000, 0, 1, 2, 1),
-    "c5b_1023": (1023, 1023, 1023, 0, 1, 2, 1),
-    "c2_mlp": "mlp",
-    "idx_data": "idx",
-}
+from fast_dl_amd.profiling import CONFIGS as _PROFILE_WORKLOADS  # noqa: E402
+
+PROFILE_CONFIGS = {name: (None if name == "headline" else
+                          (w.kind if w.shape is None else w.shape))
+                   for name, w in _PROFILE_WORKLOADS.items()}
+CLOCK_WARM = True  # --no-clock-warm turns warm_clock off (counter runs)
 
 
 def parse_args():
@@ -66,8 +57,20 @@ def parse_args():
     ap.add_argument("--profile-config", default="headline", choices=sorted(PROFILE_CONFIGS),
                     help="with --profile-mode: which BASELINE configuration to launch")
     ap.add_argument("--copy-calib", action="store_true",
-                    help="with --profile-mode: also run a 256 MiB device copy, the known-size "
-                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
+                    help="with --profile-mode: also run known-size copy, sum and fill kernels "
+                         "that scale the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--no-clock-warm", action="store_true",
+                    help="with --profile-mode: skip the clock warm-up bursts (counter runs, "
+                         "which serialize every dispatch)")
+    ap.add_argument("--collect-profiles", metavar="DIR", default=None,
+                    help="run every rocprofv3 pass of fast_dl_amd/profiling.py into DIR (each "
+                         "as a child process of this one, which does not touch the GPU)")
+    ap.add_argument("--stages", default="trace,vendor,counters",
+                    help="with --collect-profiles: comma-separated stages")
+    ap.add_argument("--configs", default=None,
+                    help="with --collect-profiles: comma-separated configurations (default all)")
+    ap.add_argument("--summarize", metavar="DIR", default=None,
+                    help="write the profiles/*.txt summaries from the rocprofv3 output in DIR")
     return ap.parse_args()
 
 
@@ -89,6 +92,8 @@ def warm_clock(fn, stream, ms=50.0, min_launch_ms=0.015):
     cost, which a long burst of launches beforehand was measured to raise."""
     import torch
 
+    if not CLOCK_WARM:
+        return
     fn()  # one-time costs (code load, first-touch) stay out of the estimate
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -122,7 +127,7 @@ def copy_calibration(torch):
     for _ in range(3):
         sdst.copy_(small)
     for _ in range(3):
-        torch.sum(big, out=out)
+        torch.sum(big, dim=0, out=out)
     for _ in range(3):
         dst.fill_(2.0)
     torch.cuda.synchronize()
@@ -590,7 +595,20 @@ def sweep(capi, torch, path):
 
 
 def main():
+    global CLOCK_WARM
     args = parse_args()
+    if args.collect_profiles or args.summarize:
+        from fast_dl_amd import profiling
+
+        if args.collect_profiles:
+            rc = profiling.collect(args.collect_profiles, args.stages.split(","),
+                                   args.configs.split(",") if args.configs else None)
+            if rc:
+                sys.exit(rc)
+        if args.summarize:
+            profiling.summarize(args.summarize)
+        return
+    CLOCK_WARM = not args.no_clock_warm
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "sharding the path over several GPUs is designed, not built", file=sys.stderr)
