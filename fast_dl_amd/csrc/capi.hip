@@ -38,7 +38,7 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int64_t ldb, int64_t strideB, float* C, int64_t ldc,
                         int64_t strideC, int64_t batch, const float* bias,
                         const float* aux, int epilogue, int kernel, void* stream) {
-    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_DMA128W8U) {
+    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_DMA64S) {
         return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
     }
     if ((transA != FDL_OP_N && transA != FDL_OP_T) ||
@@ -98,7 +98,8 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
         return fail(FDL_ERROR_NOT_SUPPORTED, "sgemm: skinny kernel needs M <= 8 and B not transposed");
     }
     if ((kern == fdl::GemmKernel::Dma256 || kern == fdl::GemmKernel::Dma128 ||
-         kern == fdl::GemmKernel::Dma64 || kern == fdl::GemmKernel::Dma128W8) &&
+         kern == fdl::GemmKernel::Dma64 || kern == fdl::GemmKernel::Dma128W8 ||
+         kern == fdl::GemmKernel::Dma64S) &&
         !fdl::dma_supported(kern, p, ta, tb, batch)) {
         return fail(FDL_ERROR_NOT_SUPPORTED,
                     "sgemm: the 16-byte direct-to-LDS kernels need K % 4 == 0 and "

@@ -26,6 +26,7 @@ const char* to_string(GemmAlgo algo) {
         case GemmAlgo::MfmaDma128W8: return "mfma_dma128w8";
         case GemmAlgo::MfmaDma64U: return "mfma_dma64u";
         case GemmAlgo::MfmaDma128W8U: return "mfma_dma128w8u";
+        case GemmAlgo::MfmaDma64S: return "mfma_dma64s";
     }
     return "unknown";
 }
@@ -45,6 +46,7 @@ int kernel_id(GemmAlgo algo) {
         case GemmAlgo::MfmaDma128W8: return FDL_KERNEL_DMA128W8;
         case GemmAlgo::MfmaDma64U: return FDL_KERNEL_DMA64U;
         case GemmAlgo::MfmaDma128W8U: return FDL_KERNEL_DMA128W8U;
+        case GemmAlgo::MfmaDma64S: return FDL_KERNEL_DMA64S;
     }
     return FDL_KERNEL_AUTO;
 }

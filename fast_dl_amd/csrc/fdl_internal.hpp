@@ -54,6 +54,7 @@ enum class GemmKernel : int {
     Dma128W8 = 11,    // 128x128x64 tile, global -> LDS copies, eight waves of 64x32
     Dma64U = 12,      // Dma64 with 4-byte copies (any K, leading dimension, alignment)
     Dma128W8U = 13,   // Dma128W8 with 4-byte copies
+    Dma64S = 14,      // 64x64x16 tile, four K-tiles in flight, four 32x32 waves
     Auto = -1,
 };
 

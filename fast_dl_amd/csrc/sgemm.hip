@@ -735,9 +735,24 @@ __device__ __forceinline__ void spread_hint(std::integer_sequence<int, J...>) {
     (spread_hint_one<kMfma, kReads, kCopies, J>(), ...);
 }
 
+// Block -> (batch, tile) for a launch whose 1-D grid covers every tile of
+// every batch (few tiles per batch): renumbered so each XCD owns one
+// contiguous range of (batch, tile) pairs, i.e. whole batches when the batch
+// count is a multiple of 8.  A batch's tiles share its operand panels, which
+// then come into one XCD's L2 once.
+__device__ __forceinline__ void flat_batch_coords(int bid, int nblocks, int tiles_m, int tiles_n,
+                                                  int& tm, int& tn, int64_t& bz) {
+    if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+    const int tiles = tiles_m * tiles_n;
+    bz = bid / tiles;
+    const int t = bid - (int)bz * tiles;
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+}
+
 template <class Cfg, bool TA, bool TB>
 __global__ void __launch_bounds__(Cfg::NT, Cfg::WPE)
-sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
+sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, WM = Cfg::WM, WN = Cfg::WN;
     constexpr int NT = Cfg::NT, S = Cfg::STAGES;
     constexpr int FM = WM / 32, FN = WN / 32, WGM = BM / WM;
@@ -768,10 +783,15 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n) {
     const int g0 = kset * NGK;                  // this set's first k-group of a tile
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    int64_t bz;
+    if (flat) {
+        flat_batch_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn, bz);
+    } else {
+        tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+        bz = blockIdx.y;
+    }
     const int m0 = tm * BM;
     const int n0 = tn * BN;
-    const int64_t bz = blockIdx.y;
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
 
@@ -1516,24 +1536,31 @@ hipError_t launch_tiled(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
     return hipGetLastError();
 }
 
+// Batched problems of at most this many tiles each run on a 1-D grid whose
+// blocks are spread so that each XCD owns whole batches (flat_batch_coords);
+// larger ones keep grid.y = batch and the per-problem tile grouping.
+constexpr int kFlatBatchMaxTiles = 64;
+
 template <class Cfg>
 hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStream_t stream) {
     const int tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     const int tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
-    const dim3 grid(tiles_m * tiles_n, nbatch);
+    const int tiles = tiles_m * tiles_n;
+    const int flat = nbatch > 1 && tiles <= kFlatBatchMaxTiles;
+    const dim3 grid = flat ? dim3(tiles * nbatch) : dim3(tiles, nbatch);
     const dim3 block(Cfg::NT);
     if (!ta && !tb) {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n);
+                           tiles_m, tiles_n, flat);
     } else if (!ta) {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, true>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n);
+                           tiles_m, tiles_n, flat);
     } else if (!tb) {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, true, false>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n);
+                           tiles_m, tiles_n, flat);
     } else {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, true, true>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n);
+                           tiles_m, tiles_n, flat);
     }
     return hipGetLastError();
 }
@@ -1767,6 +1794,10 @@ using CfgDma128W8 = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1>;
 // 4-byte-aligned pointer, at 2-3% below their 16-byte twins (1023^3: 26.5 us
 // against 44 us for split-K; 4095^3: 1.11 ms).
 using CfgDma64U = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2, 1>;
+// 64x64x16 with four stages: every 16-deep K-tile of a short-K problem is
+// copied at once and each is multiplied as soon as it lands, so a block's
+// MFMAs overlap the arrival of its later tiles (the C4 batch, K = 64).
+using CfgDma64S = DmaCfg<64, 64, 16, 32, 32, 4, 0, 1>;
 using CfgDma128W8U = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1, 1, 1>;
 
 // Dispatch cost model.  A config runs `slots` blocks per CU at full
@@ -1818,7 +1849,7 @@ bool is_dma4(GemmKernel k) {
 
 bool is_dma(GemmKernel k) {
     return k == GemmKernel::Dma256 || k == GemmKernel::Dma128 || k == GemmKernel::Dma64 ||
-           k == GemmKernel::Dma128W8 || is_dma4(k);
+           k == GemmKernel::Dma128W8 || k == GemmKernel::Dma64S || is_dma4(k);
 }
 
 // Largest leading dimension of the 4-byte-copy kernels: a copy's 32-bit
@@ -1864,6 +1895,7 @@ const char* kernel_name(GemmKernel k) {
         case GemmKernel::Dma128W8: return "dma128w8";
         case GemmKernel::Dma64U: return "dma64u";
         case GemmKernel::Dma128W8U: return "dma128w8u";
+        case GemmKernel::Dma64S: return "dma64s";
         case GemmKernel::Auto: return "auto";
     }
     return "unknown";
@@ -1913,6 +1945,10 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
             }
         }
     }
+    // K of at most 128: every 16-deep K-tile in flight at once beats one or
+    // two 64-deep tiles that must land whole (the C4 batch, 64 x 128x128x64:
+    // 5.5 vs 6.0 us from HBM).
+    if (best == GemmKernel::Dma64 && p.K <= 128) best = GemmKernel::Dma64S;
     return best;
 }
 
@@ -2020,7 +2056,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
     if (is_dma(kernel) && !dma_supported(kernel, p0, transA, transB, batch)) {
         if (!automatic) return hipErrorInvalidValue;
         // Misaligned pointers: the 4-byte-copy tile, else the register-staged one.
-        const GemmKernel u = kernel == GemmKernel::Dma64 ? GemmKernel::Dma64U : GemmKernel::Dma128W8U;
+        const GemmKernel u = (kernel == GemmKernel::Dma64 || kernel == GemmKernel::Dma64S)
+                                 ? GemmKernel::Dma64U
+                                 : GemmKernel::Dma128W8U;
         if (!is_dma4(kernel) && dma_supported(u, p0, transA, transB, batch)) {
             kernel = u;
         } else {
@@ -2085,6 +2123,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             case GemmKernel::Dma128W8U:
                 err = launch_dma<CfgDma128W8U>(p, transA, transB, nb, stream);
+                break;
+            case GemmKernel::Dma64S:
+                err = launch_dma<CfgDma64S>(p, transA, transB, nb, stream);
                 break;
             default:
                 return hipErrorInvalidValue;

@@ -26,6 +26,7 @@ enum class GemmAlgo {
     MfmaDma128W8,   // 128x128x64 tile, same copies, eight waves, one block per CU
     MfmaDma64U,     // MfmaDma64 with 4-byte copies: any k, leading dimension, alignment
     MfmaDma128W8U,  // MfmaDma128W8 with 4-byte copies
+    MfmaDma64S,     // 64x64x16 tile, same copies as MfmaDma64, all K-tiles in flight (k <= 128)
 };
 
 const char* to_string(GemmAlgo algo);

@@ -108,7 +108,9 @@ typedef enum fdl_kernel {
     FDL_KERNEL_DMA64U = 12,    /* FDL_KERNEL_DMA64 with 4-byte copies: any K, any
                                   leading dimension up to 2^24, any 4-byte-aligned
                                   operand (odd shapes, unaligned views)            */
-    FDL_KERNEL_DMA128W8U = 13  /* FDL_KERNEL_DMA128W8 with 4-byte copies          */
+    FDL_KERNEL_DMA128W8U = 13, /* FDL_KERNEL_DMA128W8 with 4-byte copies          */
+    FDL_KERNEL_DMA64S = 14     /* 64x64x16 tile, 16-byte copies, four K-tiles in
+                                  flight, four 32x32 waves: short-K batches       */
 } fdl_kernel;
 
 /*

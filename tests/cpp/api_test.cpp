@@ -150,7 +150,8 @@ int main() {
         auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
         for (auto algo : {dl::kernels::GemmAlgo::MfmaDma256, dl::kernels::GemmAlgo::MfmaDma128,
                           dl::kernels::GemmAlgo::MfmaDma64, dl::kernels::GemmAlgo::MfmaDma128W8,
-                          dl::kernels::GemmAlgo::MfmaDma64U, dl::kernels::GemmAlgo::MfmaDma128W8U}) {
+                          dl::kernels::GemmAlgo::MfmaDma64U, dl::kernels::GemmAlgo::MfmaDma128W8U,
+                          dl::kernels::GemmAlgo::MfmaDma64S}) {
             dl::Tensor tc(dl::Shape({m, n}), dl::DType::Float32, kDev);
             dl::kernels::gemm(static_cast<const float*>(ta.data()),
                               static_cast<const float*>(tb.data()), static_cast<float*>(tc.data()),

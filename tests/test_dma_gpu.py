@@ -1,7 +1,6 @@
-"""GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256, K-tile 16;
-FDL_KERNEL_DMA128, K-tile 32; FDL_KERNEL_DMA64 and FDL_KERNEL_DMA128W8, K-tile
-64) and of their
-dispatch rules: they run where K is a multiple of 4 (a partial last K-tile is
+"""GPU parity of the direct-to-LDS kernels (FDL_KERNEL_DMA256 and
+FDL_KERNEL_DMA64S, K-tile 16; FDL_KERNEL_DMA128, K-tile 32; FDL_KERNEL_DMA64
+and FDL_KERNEL_DMA128W8, K-tile 64) and of their dispatch rules: they run where K is a multiple of 4 (a partial last K-tile is
 clamped and masked) and both operands are 16-byte vectorisable, refuse other
 problems with FDL_ERROR_NOT_SUPPORTED when forced, and the automatic choice
 falls back to the register-staged kernel with the same tile for misaligned
@@ -16,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 DMA = capi.KERNEL_DMA256
 DMAS16 = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32), (capi.KERNEL_DMA64, 64),
-          (capi.KERNEL_DMA128W8, 64)]
+          (capi.KERNEL_DMA128W8, 64), (capi.KERNEL_DMA64S, 16)]
 # The 4-byte-copy twins run every aligned case too (their own odd-shape cases
 # are in test_dma4_gpu.py).
 DMAS = DMAS16 + [(capi.KERNEL_DMA64U, 64), (capi.KERNEL_DMA128W8U, 64)]
@@ -81,6 +80,35 @@ def test_dma_batched_and_padded_ld(device, fam, bk):
     Bp[:, :, :K] = B
     c = gpu_sgemm(0, 1, Ap, Bp, M, N, K, batch=batch, kernel=fam, lda=lda, ldb=ldb, ldc=ldc)
     check_gemm(c, 0, 1, A, B, M, N, K, batch=batch)
+
+
+@pytest.mark.parametrize("fam,bk", DMAS)
+@pytest.mark.parametrize("batch", [2, 8, 13, 64])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_dma_flat_batch_grid(device, fam, bk, batch, tb):
+    # Problems of at most 64 tiles each run on a 1-D grid of batch x tiles
+    # blocks, renumbered so each XCD owns whole batches when the block count
+    # is a multiple of 8 (batch 8 and 64 here; 2 and 13 keep the plain order).
+    # A broadcast B (batch stride 0) and padded leading dimensions check the
+    # per-batch offsets; C is pre-filled with NaN to catch unwritten tiles.
+    import torch
+
+    M, N, K = 136, 100, 48
+    g = _rng(31, batch, tb, fam)
+    lda, ldb, ldc = K + 4, (K if tb else N) + 8, N + 4
+    A = g.standard_normal((batch, M, lda)).astype(np.float32)
+    B = g.standard_normal((1, N if tb else K, ldb)).astype(np.float32)
+    dA, dB = dev(A), dev(B)
+    dC = torch.full((batch, M, ldc), float("nan"), device="cuda")
+    say(f"dma flat batch fam={fam} batch={batch} tb={tb}")
+    capi.sgemm_ex_select(0, tb, M, N, K, dA.data_ptr(), lda, M * lda, dB.data_ptr(), ldb, 0,
+                         dC.data_ptr(), ldc, M * ldc, batch, None, None, 0, fam, stream())
+    c = host(dC)
+    assert np.all(np.isnan(c[:, :, N:])), "wrote outside the ldc window"
+    Ap = np.ascontiguousarray(A[:, :, :K])
+    Bv = B[:, :, :K] if tb else B[:, :, :N]
+    Bp = np.ascontiguousarray(np.broadcast_to(Bv, (batch,) + Bv.shape[1:]))
+    check_gemm(np.ascontiguousarray(c[:, :, :N]), 0, tb, Ap, Bp, M, N, K, batch=batch)
 
 
 def _raw_select(ta, tb, M, N, K, a_ptr, lda, b_ptr, ldb, c_ptr, kernel):

@@ -145,7 +145,8 @@ def test_config4_batched(device, tb):
     g = rng(4)
     batch, M, K, N = 64, 128, 64, 128
     A, B = _ops(g, 0, tb, M, N, K, batch, scale=np.sqrt(1 / 8))
-    for fam in FAMILIES + [capi.KERNEL_AUTO]:
+    for fam in FAMILIES + [capi.KERNEL_DMA64, capi.KERNEL_DMA64S, capi.KERNEL_DMA64U,
+                           capi.KERNEL_AUTO]:
         say(f"config4 tb={tb} fam={fam}")
         c = gpu_sgemm(0, tb, A, B, M, N, K, batch=batch, kernel=fam)
         check_gemm(c, 0, tb, A, B, M, N, K, batch=batch, fp32_oracle=(fam == capi.KERNEL_AUTO))
