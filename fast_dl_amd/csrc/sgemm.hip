@@ -76,21 +76,23 @@ __device__ __forceinline__ void store_epilogue(float v, const GemmParams& p,
 
 // The operand an epilogue reads besides the accumulator (bias[j], aux[off] or
 // upd[off]), loaded before the K loop so its latency overlaps the MFMAs.
+// One unconditional load through a pointer chosen by the (uniform)
+// epilogue: a switch around several loads compiles to exec-masked branches
+// that load into one register, and the compiler then waits for the first
+// load before anything after it, the K loop's loads included.  Without an
+// operand the load reads C[off] (off must be a valid element) and the value
+// is not used.
 __device__ __forceinline__ float epilogue_operand(const GemmParams& p,
+                                                  const float* __restrict__ C,
                                                   const float* __restrict__ aux,
                                                   const float* __restrict__ upd, int64_t off,
                                                   int j) {
-    switch (p.epilogue) {
-        case EPI_BIAS:
-        case EPI_BIAS_RELU:
-            return p.bias[j];
-        case EPI_RELU_GRAD:
-            return aux[off];
-        case EPI_SGD:
-            return upd[off];
-        default:
-            return 0.0f;
-    }
+    const int e = p.epilogue;
+    const float* src = (e == EPI_BIAS || e == EPI_BIAS_RELU) ? p.bias + j
+                       : e == EPI_RELU_GRAD                  ? aux + off
+                       : e == EPI_SGD                        ? upd + off
+                                                             : C + off;
+    return *src;
 }
 
 // store_epilogue with the extra operand already loaded (epilogue_operand).
@@ -1186,11 +1188,14 @@ __device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, 
         const int e = tid + q * KW * kWave;
         const int r = e / kWave;
         const int ln = e % kWave;
-        const int gi = m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
-        const int gj = n0 + (ln & 31);
-        pre[q] = (e < 16 * kWave && gi < p.M && gj < p.N)
-                     ? epilogue_operand(p, aux, upd, (int64_t)gi * p.ldc + gj, gj)
-                     : 0.0f;
+        // Clamped into C rather than branched around: a lane-divergent branch
+        // around the load makes both of its sides load into one register,
+        // and the compiler then waits for the first before the K loop's
+        // loads are even issued.  Out-of-range lanes load a valid element
+        // they never store.
+        const int gi = min(m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), p.M - 1);
+        const int gj = min(n0 + (ln & 31), p.N - 1);
+        pre[q] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
     }
 
     floatx16 acc;
@@ -1312,11 +1317,10 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
         const int e = tid + u * KW * kWave;
         const int r = e / kWave;
         const int ln = e % kWave;
-        const int gi = m0 + 4 * (ln >> 4) + r;
-        const int gj = n0 + (ln & 15);
-        pre[u] = (e < 4 * kWave && gi < p.M && gj < p.N)
-                     ? epilogue_operand(p, aux, upd, (int64_t)gi * p.ldc + gj, gj)
-                     : 0.0f;
+        // Clamped, not branched around (see splitk32_body).
+        const int gi = min(m0 + 4 * (ln >> 4) + r, p.M - 1);
+        const int gj = min(n0 + (ln & 15), p.N - 1);
+        pre[u] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
     }
 
     const int row = min(m0 + i, p.M - 1);
