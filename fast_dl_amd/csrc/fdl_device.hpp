@@ -26,8 +26,18 @@ __device__ __forceinline__ void colsum_body(const float* __restrict__ x, float* 
     const int grp = threadIdx.x / kColsumCols;
     const int64_t c = block * (int64_t)kColsumCols + cl;
     const int64_t cc = c < cols ? c : cols - 1;  // clamped: loads stay in bounds
+    // Rows are added in order (grp, grp + 8, grp + 16, ...); the loads of
+    // 32 of them are in flight at once, so a 256-row matrix costs one
+    // round trip to memory instead of four.
     float s = 0.0f;
     int64_t r = grp;
+    for (; r + 31 * kColsumGroups < rows; r += 32 * kColsumGroups) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = x[(r + u * kColsumGroups) * cols + cc];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) s += v[u];
+    }
     for (; r + 7 * kColsumGroups < rows; r += 8 * kColsumGroups) {
         float v[8];
 #pragma unroll
@@ -62,8 +72,16 @@ __device__ __forceinline__ void xent_finalize_body(const float* __restrict__ par
     const int t = threadIdx.x;
     if (t > classes) return;
     const int stride = classes + 1;
+    // Records in block order, 32 of them in flight at once.
     float s = 0.0f;
     int b = 0;
+    for (; b + 32 <= nparts; b += 32) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = part[(b + u) * stride + t];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) s += v[u];
+    }
     for (; b + 8 <= nparts; b += 8) {
         float v[8];
 #pragma unroll

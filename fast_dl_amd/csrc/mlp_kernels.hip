@@ -283,16 +283,18 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
     const int row = blockIdx.x * kHeadRows + rl;
     const bool live = row < batch;
     const int rowc = live ? row : batch - 1;  // clamped: loads stay in bounds
+    // Every global load below is issued unconditionally at an address
+    // clamped into its array, and values outside the problem are zeroed by
+    // a select after the load: a load under a lane-divergent branch makes
+    // the compiler wait for it before issuing the ones after it, which
+    // turned the staging into two dependent round trips.
     const int64_t label = labels[rowc];
     const float* hrow = H + (int64_t)rowc * hidden;
     float h[NH];
 #pragma unroll
-    for (int k = 0; k < NH; ++k) {
-        const int j = lane + 32 * k;
-        h[k] = j < hidden ? hrow[j] : 0.0f;
-    }
-    if (t < CM) b2s[t] = t < classes ? b2[t] : 0.0f;
-    // Sixteen loads in flight per thread before their LDS stores.
+    for (int k = 0; k < NH; ++k) h[k] = hrow[min(lane + 32 * k, hidden - 1)];
+    const float b2v = b2[min(t, classes - 1)];
+    // W2 in batches of sixteen loads in flight per thread.
 #pragma unroll
     for (int b0 = 0; b0 < kPerThread; b0 += 16) {
         float v[16];
@@ -300,14 +302,18 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
         for (int u = 0; u < 16; ++u) {
             const int e = (b0 + u) * kBlock + t;
             const int j = e / CM, c = e % CM;
-            v[u] = (j < hidden && c < classes) ? W2[j * classes + c] : 0.0f;
+            v[u] = W2[min(j, hidden - 1) * classes + min(c, classes - 1)];
         }
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int e = (b0 + u) * kBlock + t;
-            w2s[(e / CM) * LR + e % CM] = v[u];
+            const int j = e / CM, c = e % CM;
+            w2s[j * LR + c] = (j < hidden && c < classes) ? v[u] : 0.0f;
         }
     }
+#pragma unroll
+    for (int k = 0; k < NH; ++k) h[k] = lane + 32 * k < hidden ? h[k] : 0.0f;
+    if (t < CM) b2s[t] = t < classes ? b2v : 0.0f;
     __syncthreads();
 
     float z[CM];

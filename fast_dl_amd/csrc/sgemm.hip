@@ -1631,7 +1631,7 @@ struct GroupArgs {
 };
 
 constexpr int kGroupKW = 4;   // split-K waves of a grouped GEMM job (256 threads)
-constexpr int kGroupITS = 2;
+constexpr int kGroupITS = 8;  // 64 k of loads per wave in flight (MLP step 22.5 -> 21.9 us)
 
 template <bool TA, bool TB, bool VA, bool VB>
 struct JobGemm {
