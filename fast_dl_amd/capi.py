@@ -15,13 +15,14 @@ EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_BIAS_RELU, EPILOGUE_RELU, EPILOGUE_RELU_G
 KERNEL_AUTO, KERNEL_TILED128, KERNEL_TILED64, KERNEL_SPLITK32, KERNEL_SKINNY = -1, 0, 1, 2, 3
 KERNEL_TILED256, KERNEL_TILED256X128, KERNEL_TILED128W8, KERNEL_SPLITK16 = 4, 5, 6, 7
 KERNEL_DMA256, KERNEL_DMA128, KERNEL_DMA64, KERNEL_DMA128W8 = 8, 9, 10, 11
-KERNEL_DMA64U, KERNEL_DMA128W8U, KERNEL_DMA64S = 12, 13, 14
+KERNEL_DMA64U, KERNEL_DMA128W8U, KERNEL_DMA64S, KERNEL_DMA96X32U = 12, 13, 14, 15
 KERNEL_NAMES = {KERNEL_TILED128: "tiled128", KERNEL_TILED64: "tiled64",
                 KERNEL_SPLITK32: "splitk32", KERNEL_SKINNY: "skinny", KERNEL_TILED256: "tiled256",
                 KERNEL_TILED256X128: "tiled256x128", KERNEL_TILED128W8: "tiled128w8",
                 KERNEL_SPLITK16: "splitk16", KERNEL_DMA256: "dma256", KERNEL_DMA128: "dma128",
                 KERNEL_DMA64: "dma64", KERNEL_DMA128W8: "dma128w8", KERNEL_DMA64U: "dma64u",
-                KERNEL_DMA128W8U: "dma128w8u", KERNEL_DMA64S: "dma64s"}
+                KERNEL_DMA128W8U: "dma128w8u", KERNEL_DMA64S: "dma64s",
+                KERNEL_DMA96X32U: "dma96x32u"}
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _LIB = None

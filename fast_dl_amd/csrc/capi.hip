@@ -38,7 +38,7 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int64_t ldb, int64_t strideB, float* C, int64_t ldc,
                         int64_t strideC, int64_t batch, const float* bias,
                         const float* aux, int epilogue, int kernel, void* stream) {
-    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_DMA64S) {
+    if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_DMA96X32U) {
         return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
     }
     if ((transA != FDL_OP_N && transA != FDL_OP_T) ||
@@ -105,7 +105,8 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                     "sgemm: the 16-byte direct-to-LDS kernels need K % 4 == 0 and "
                     "16-byte-vectorisable operands");
     }
-    if ((kern == fdl::GemmKernel::Dma64U || kern == fdl::GemmKernel::Dma128W8U) &&
+    if ((kern == fdl::GemmKernel::Dma64U || kern == fdl::GemmKernel::Dma128W8U ||
+         kern == fdl::GemmKernel::Dma96x32U) &&
         !fdl::dma_supported(kern, p, ta, tb, batch)) {
         return fail(FDL_ERROR_NOT_SUPPORTED,
                     "sgemm: the 4-byte direct-to-LDS kernels need leading dimensions up to 2^24 "

@@ -27,6 +27,7 @@ const char* to_string(GemmAlgo algo) {
         case GemmAlgo::MfmaDma64U: return "mfma_dma64u";
         case GemmAlgo::MfmaDma128W8U: return "mfma_dma128w8u";
         case GemmAlgo::MfmaDma64S: return "mfma_dma64s";
+        case GemmAlgo::MfmaDma96x32U: return "mfma_dma96x32u";
     }
     return "unknown";
 }
@@ -47,6 +48,7 @@ int kernel_id(GemmAlgo algo) {
         case GemmAlgo::MfmaDma64U: return FDL_KERNEL_DMA64U;
         case GemmAlgo::MfmaDma128W8U: return FDL_KERNEL_DMA128W8U;
         case GemmAlgo::MfmaDma64S: return FDL_KERNEL_DMA64S;
+        case GemmAlgo::MfmaDma96x32U: return FDL_KERNEL_DMA96X32U;
     }
     return FDL_KERNEL_AUTO;
 }

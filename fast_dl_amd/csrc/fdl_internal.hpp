@@ -55,6 +55,7 @@ enum class GemmKernel : int {
     Dma64U = 12,      // Dma64 with 4-byte copies (any K, leading dimension, alignment)
     Dma128W8U = 13,   // Dma128W8 with 4-byte copies
     Dma64S = 14,      // 64x64x16 tile, four K-tiles in flight, four 32x32 waves
+    Dma96x32U = 15,   // 96x32x64 tile, 4-byte copies, four sets of three 32x32 waves
     Auto = -1,
 };
 

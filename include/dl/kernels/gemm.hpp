@@ -27,6 +27,7 @@ enum class GemmAlgo {
     MfmaDma64U,     // MfmaDma64 with 4-byte copies: any k, leading dimension, alignment
     MfmaDma128W8U,  // MfmaDma128W8 with 4-byte copies
     MfmaDma64S,     // 64x64x16 tile, same copies as MfmaDma64, all K-tiles in flight (k <= 128)
+    MfmaDma96x32U,  // 96x32x64 tile, 4-byte copies, twelve waves (mid sizes short of tiles)
 };
 
 const char* to_string(GemmAlgo algo);

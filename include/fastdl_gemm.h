@@ -109,8 +109,11 @@ typedef enum fdl_kernel {
                                   leading dimension up to 2^24, any 4-byte-aligned
                                   operand (odd shapes, unaligned views)            */
     FDL_KERNEL_DMA128W8U = 13, /* FDL_KERNEL_DMA128W8 with 4-byte copies          */
-    FDL_KERNEL_DMA64S = 14     /* 64x64x16 tile, 16-byte copies, four K-tiles in
+    FDL_KERNEL_DMA64S = 14,    /* 64x64x16 tile, 16-byte copies, four K-tiles in
                                   flight, four 32x32 waves: short-K batches       */
+    FDL_KERNEL_DMA96X32U = 15  /* 96x32x64 tile, 4-byte copies, four k-group sets
+                                  of three 32x32 waves: mid sizes whose 64x64
+                                  tiles leave CUs idle                            */
 } fdl_kernel;
 
 /*

@@ -151,7 +151,7 @@ int main() {
         for (auto algo : {dl::kernels::GemmAlgo::MfmaDma256, dl::kernels::GemmAlgo::MfmaDma128,
                           dl::kernels::GemmAlgo::MfmaDma64, dl::kernels::GemmAlgo::MfmaDma128W8,
                           dl::kernels::GemmAlgo::MfmaDma64U, dl::kernels::GemmAlgo::MfmaDma128W8U,
-                          dl::kernels::GemmAlgo::MfmaDma64S}) {
+                          dl::kernels::GemmAlgo::MfmaDma64S, dl::kernels::GemmAlgo::MfmaDma96x32U}) {
             dl::Tensor tc(dl::Shape({m, n}), dl::DType::Float32, kDev);
             dl::kernels::gemm(static_cast<const float*>(ta.data()),
                               static_cast<const float*>(tb.data()), static_cast<float*>(tc.data()),
@@ -174,7 +174,8 @@ int main() {
             // ... while the 4-byte-copy twins take it.
             const auto want2 = host_gemm(a2.to_host<float>(), b2.to_host<float>(), m, n, k2);
             for (auto algo : {dl::kernels::GemmAlgo::MfmaDma64U,
-                              dl::kernels::GemmAlgo::MfmaDma128W8U}) {
+                              dl::kernels::GemmAlgo::MfmaDma128W8U,
+                              dl::kernels::GemmAlgo::MfmaDma96x32U}) {
                 dl::kernels::gemm(static_cast<const float*>(a2.data()),
                                   static_cast<const float*>(b2.data()),
                                   static_cast<float*>(c2.data()), m, n, k2, algo);

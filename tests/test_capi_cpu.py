@@ -75,7 +75,7 @@ def test_other_entry_points_validate():
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 1, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
                          1, None, None, 0, 3, None) == -2  # skinny with B transposed
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 16, 1, 16, 0, 1, 16, 0, 1, 16, 0,
-                         1, None, None, 0, 15, None) == -1
+                         1, None, None, 0, 16, None) == -1
     assert capi.raw_call("fdl_sgemm_ex_select", 0, 0, 16, 16, 22, 1 << 20, 24, 0, 1 << 20, 16, 0,
                          1 << 20, 16, 0, 1, None, None, 0, capi.KERNEL_DMA256, None) == -2
     assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
@@ -95,7 +95,9 @@ def test_kernel_choice():
     assert capi.kernel_choice(0, 0, 1024, 1024, 1024) == capi.KERNEL_DMA64
     assert capi.kernel_choice(0, 0, 1000, 1000, 1000) == capi.KERNEL_DMA64
     assert capi.kernel_choice(0, 0, 1023, 1023, 1023) == capi.KERNEL_DMA64U
-    assert capi.kernel_choice(0, 0, 777, 777, 777) == capi.KERNEL_DMA64U
+    # 777^3: 169 tiles of 64x64 leave 87 CUs idle; 225 tiles of 96x32 do not
+    assert capi.kernel_choice(0, 0, 777, 777, 777) == capi.KERNEL_DMA96X32U
+    assert capi.kernel_choice(0, 0, 700, 900, 800) == capi.KERNEL_DMA96X32U
     # short K: a full GPU of 64x64 tiles takes the four-stage 64x64x16 tile
     # (the C4 batch), a tile count just past one round stays on split-K
     assert capi.kernel_choice(0, 0, 128, 128, 64, 64) == capi.KERNEL_DMA64S

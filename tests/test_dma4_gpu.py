@@ -1,4 +1,5 @@
 """GPU parity of the 4-byte-copy direct-to-LDS kernels (FDL_KERNEL_DMA64U,
+FDL_KERNEL_DMA96X32U,
 FDL_KERNEL_DMA128W8U) on the problems the 16-byte ones refuse: any K (partial
 last K-tile of any length), odd M and N, odd leading dimensions and batch
 strides, operands one float off a 16-byte boundary; with every epilogue; and
@@ -11,7 +12,7 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, s
 
 pytestmark = pytest.mark.gpu
 
-DMA4 = [capi.KERNEL_DMA64U, capi.KERNEL_DMA128W8U]
+DMA4 = [capi.KERNEL_DMA64U, capi.KERNEL_DMA128W8U, capi.KERNEL_DMA96X32U]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 ODD = [(1, 1, 1), (3, 5, 7), (65, 63, 129), (130, 258, 67), (200, 136, 1023), (257, 129, 65)]
 
@@ -87,11 +88,12 @@ def test_dma4_epilogues(device, fam, epi):
     check_gemm(c, 0, 0, A, B, M, N, K, bias=bias, aux=aux, epilogue=epi)
 
 
-@pytest.mark.parametrize("n", [777, 1023])
-def test_auto_odd_cubes(device, n):
-    # C5b's odd cubes go to the 4-byte-copy 64x64 tile, with the fused
-    # bias+ReLU epilogue.
-    assert capi.kernel_choice(0, 0, n, n, n) == capi.KERNEL_DMA64U
+@pytest.mark.parametrize("n,fam", [(777, capi.KERNEL_DMA96X32U), (1023, capi.KERNEL_DMA64U)])
+def test_auto_odd_cubes(device, n, fam):
+    # C5b's odd cubes go to the 4-byte-copy tiles, with the fused bias+ReLU
+    # epilogue: 777^3 to the 96x32 tile (225 tiles fill the GPU where 169
+    # 64x64 ones do not), 1023^3 to the 64x64 one.
+    assert capi.kernel_choice(0, 0, n, n, n) == fam
     g = _rng(n, 3)
     A, B = operands(g, 0, 0, n, n, n, 1)
     bias = g.standard_normal(n).astype(np.float32)

@@ -18,7 +18,8 @@ DMAS16 = [(capi.KERNEL_DMA256, 16), (capi.KERNEL_DMA128, 32), (capi.KERNEL_DMA64
           (capi.KERNEL_DMA128W8, 64), (capi.KERNEL_DMA64S, 16)]
 # The 4-byte-copy twins run every aligned case too (their own odd-shape cases
 # are in test_dma4_gpu.py).
-DMAS = DMAS16 + [(capi.KERNEL_DMA64U, 64), (capi.KERNEL_DMA128W8U, 64)]
+DMAS = DMAS16 + [(capi.KERNEL_DMA64U, 64), (capi.KERNEL_DMA128W8U, 64),
+                 (capi.KERNEL_DMA96X32U, 64)]
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 # M and N multiples of 4 (either may be the contiguous extent), ragged against
 # the tiles; K in K-tiles (16 or 32 each) covering 1, 2, 3 and many K-tiles.
@@ -164,7 +165,7 @@ def test_dma_refuses_unsupported_problems(device):
         assert _raw_select(0, 0, 64, 64, 32, p, 33, p, 64, p, fam) == -2
         # N (B's contiguous extent) not a multiple of 4
         assert _raw_select(0, 0, 64, 66, 32, p, 32, p, 66, p, fam) == -2
-    for fam in (capi.KERNEL_DMA64U, capi.KERNEL_DMA128W8U):
+    for fam in (capi.KERNEL_DMA64U, capi.KERNEL_DMA128W8U, capi.KERNEL_DMA96X32U):
         # leading dimension past 2^24
         assert _raw_select(0, 0, 64, 64, 32, p, (1 << 24) + 1, p, 64, p, fam) == -2
         assert "4-byte" in capi.last_error()

@@ -211,7 +211,7 @@ def test_config5_non_tile_multiples(device, n):
     g = rng(n)
     A, B = _ops(g, 0, 0, n, n, n, 1)
     bias = (g.standard_normal(n) * 0.1).astype(np.float32)
-    for fam in FAMILIES + [capi.KERNEL_AUTO]:
+    for fam in FAMILIES + [capi.KERNEL_DMA64U, capi.KERNEL_DMA96X32U, capi.KERNEL_AUTO]:
         say(f"config5b n={n} fam={fam}")
         c = gpu_sgemm(0, 0, A, B, n, n, n, bias=bias, epilogue=capi.EPILOGUE_BIAS_RELU,
                       kernel=fam)
