@@ -238,28 +238,90 @@ softmax_xent_db_sgd_kernel(const float* __restrict__ logits,
 // The block's record at part + block * (classes + 1): the column sums of its
 // G2 rows (rows in order), then the sum of its rows' loss shares;
 // xent_finalize_body adds the records in block order.
-// Sum over the 32 lanes of a half-wave; every lane gets the same value (each
-// step adds the same two operands on both lanes of a pair, in either order).
-// Lanes are paired by quad permutations, then the 8- and 16-lane mirrors
-// (which pair the groups made uniform by the steps before), then xor 16.
+// Lane exchanges within a half-wave (32 lanes) for the head's reductions.
+// Step 0 pairs lane i with i ^ 16 (ds_swizzle), step 1 with 15 - i within
+// 16 lanes (DPP row_mirror), step 2 with 7 - i within 8 (row_half_mirror),
+// steps 3 and 4 with i ^ 2 and i ^ 1 (quad permutations).  Step s always
+// pairs lanes that differ in bit 4 - s and agree in the bits above it, so
+// applying op(x, partner(x)) for s = 0..4 reduces over all 32 lanes and
+// leaves the same value on every lane (each pair computes a op b and b op a).
 template <int kCtrl>
 __device__ __forceinline__ float dpp_mov(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
                                                                  kCtrl, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float half_wave_sum(float v) {
-    constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1, 0, 3, 2]
-    constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2, 3, 0, 1]
-    constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7 - i of each 8
-    constexpr int kMirror = 0x140;      // row_mirror: lane i <-> 15 - i of each 16
-    constexpr int kXor16 = 0x401F;      // ds_swizzle bit mode: and 0x1f, xor 0x10
-    v += dpp_mov<kQuadSwap1>(v);
-    v += dpp_mov<kQuadSwap2>(v);
-    v += dpp_mov<kHalfMirror>(v);
-    v += dpp_mov<kMirror>(v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), kXor16));
-    return v;
+template <int kStep>
+__device__ __forceinline__ float half_wave_partner(float x) {
+    if constexpr (kStep == 0) {
+        constexpr int kXor16 = 0x401F;  // ds_swizzle bit mode: and 0x1f, xor 0x10
+        return __builtin_bit_cast(float,
+                                  __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), kXor16));
+    } else if constexpr (kStep == 1) {
+        return dpp_mov<0x140>(x);  // row_mirror
+    } else if constexpr (kStep == 2) {
+        return dpp_mov<0x141>(x);  // row_half_mirror
+    } else if constexpr (kStep == 3) {
+        return dpp_mov<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    } else {
+        return dpp_mov<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    }
+}
+
+__device__ __forceinline__ float half_wave_max(float x) {
+    x = fmaxf(x, half_wave_partner<0>(x));
+    x = fmaxf(x, half_wave_partner<1>(x));
+    x = fmaxf(x, half_wave_partner<2>(x));
+    x = fmaxf(x, half_wave_partner<3>(x));
+    return fmaxf(x, half_wave_partner<4>(x));
+}
+
+__device__ __forceinline__ float half_wave_sum(float x) {
+    x += half_wave_partner<0>(x);
+    x += half_wave_partner<1>(x);
+    x += half_wave_partner<2>(x);
+    x += half_wave_partner<3>(x);
+    return x + half_wave_partner<4>(x);
+}
+
+// One step of the transposing reduction: each lane holds N partial sums
+// (one per class of its current set); it keeps the lower or upper half of
+// the set (by the lane bit this step's pairing splits on) and adds the
+// partner's partial sums of the same half.  Each lane sends the half its
+// partner keeps, so a step costs N/2 exchanges.
+template <int kStep, int N>
+__device__ __forceinline__ void transpose_step(float (&v)[N], int lane) {
+    constexpr int kHalf = N / 2;
+    const bool upper = (lane >> (4 - kStep)) & 1;
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i) {
+        const float send = upper ? v[i] : v[kHalf + i];
+        const float keep = upper ? v[kHalf + i] : v[i];
+        v[i] = keep + half_wave_partner<kStep>(send);
+    }
+}
+
+// Sums CM per-lane partials over the 32 lanes of a half-wave, class by
+// class, leaving each lane with one class's total: class lane & 31 for
+// CM = 32, class (lane & 31) >> 1 for CM = 16 (lanes 2c and 2c + 1 hold the
+// same total).  31 (or 16) exchanges instead of 5 per class.
+template <int CM>
+__device__ __forceinline__ float transpose_sum(float (&v)[CM], int lane) {
+    static_assert(CM == 16 || CM == 32, "16 or 32 classes");
+    if constexpr (CM == 32) {
+        transpose_step<0, 32>(v, lane);
+        transpose_step<1, 16>(*reinterpret_cast<float(*)[16]>(v), lane);
+        transpose_step<2, 8>(*reinterpret_cast<float(*)[8]>(v), lane);
+        transpose_step<3, 4>(*reinterpret_cast<float(*)[4]>(v), lane);
+        transpose_step<4, 2>(*reinterpret_cast<float(*)[2]>(v), lane);
+        return v[0];
+    } else {
+        transpose_step<0, 16>(v, lane);
+        transpose_step<1, 8>(*reinterpret_cast<float(*)[8]>(v), lane);
+        transpose_step<2, 4>(*reinterpret_cast<float(*)[4]>(v), lane);
+        transpose_step<3, 2>(*reinterpret_cast<float(*)[2]>(v), lane);
+        return v[0] + half_wave_partner<4>(v[0]);
+    }
 }
 
 template <int CM, int NH>
@@ -325,55 +387,48 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
 #pragma unroll
         for (int c = 0; c < CM; ++c) z[c] = fmaf(h[k], w[c], z[c]);
     }
-#pragma unroll
-    for (int c = 0; c < CM; ++c) z[c] = half_wave_sum(z[c]);
-
-    float g[CM];
+    // Each lane ends with one class's logit: class c of lane (c for CM = 32,
+    // lanes 2c and 2c + 1 for CM = 16).  The softmax runs on that class
+    // alone; the row's maximum, exponent sum and label logit are half-wave
+    // reductions.  Lanes of padded classes (c >= classes) hold 0 and take
+    // no part.
+    const int c = CM == 32 ? lane : lane >> 1;
+    const bool owner = CM == 32 || (lane & 1) == 0;  // counts class c once
+    const bool cls = c < classes;
+    float zc = transpose_sum<CM>(z, lane);
+    float gc;
     float loss_share = 0.0f;
     {
 #pragma clang fp contract(off)
         const float inv_b = 1.0f / (float)batch;
-#pragma unroll
-        for (int c = 0; c < CM; ++c) z[c] = z[c] + b2s[c];
-        float mx = z[0];
-#pragma unroll
-        for (int c = 1; c < CM; ++c) mx = c < classes ? fmaxf(mx, z[c]) : mx;
-        float s = 0.0f;
-        float ez[CM];
-#pragma unroll
-        for (int c = 0; c < CM; ++c) {
-            ez[c] = c < classes ? expf(z[c] - mx) : 0.0f;
-            s += c < classes ? ez[c] : 0.0f;
-        }
+        zc = zc + b2s[c];
+        const float mx = half_wave_max(cls ? zc : -INFINITY);
+        const float ez = cls ? expf(zc - mx) : 0.0f;
+        const float s = half_wave_sum(owner ? ez : 0.0f);
         const bool valid = label >= 0 && label < classes;
-        float zl = 0.0f;
-#pragma unroll
-        for (int c = 0; c < CM; ++c) zl = c == label ? z[c] : zl;
+        const float zl = half_wave_sum(owner && c == label ? zc : 0.0f);
         if (valid && live) loss_share = (logf(s) + mx - zl) * inv_b;
         const float inv_s = 1.0f / s;
-#pragma unroll
-        for (int c = 0; c < CM; ++c) {
-            float pc = c < classes ? ez[c] * inv_s : 0.0f;
-            if (valid && c == label) pc -= 1.0f;
-            g[c] = pc * inv_b;
-        }
+        float pc = cls ? ez * inv_s : 0.0f;
+        if (valid && c == label) pc -= 1.0f;
+        gc = pc * inv_b;
     }
-    // Lane c writes class c of the row.
-    float zsel = 0.0f, gsel = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CM; ++c) {
-        zsel = c == lane ? z[c] : zsel;
-        gsel = c == lane ? g[c] : gsel;
-    }
-    if (lane < classes) {
+    if (owner && cls) {
         if (live) {
-            logits[(int64_t)row * classes + lane] = zsel;
-            G2[(int64_t)row * classes + lane] = gsel;
+            logits[(int64_t)row * classes + c] = zc;
+            G2[(int64_t)row * classes + c] = gc;
         }
-        g2s[rl][lane] = live ? gsel : 0.0f;
+        g2s[rl][c] = live ? gc : 0.0f;
     }
     if (lane == 0) ls[rl] = loss_share;
+    if (owner && !cls && c < CM) g2s[rl][c] = 0.0f;  // padded classes of the row
+    __syncthreads();
 
+    // G1 = (G2 W2^T) * [H > 0]: the row's G2 comes back from LDS as
+    // broadcast reads, summed in class order.
+    float g[CM];
+#pragma unroll
+    for (int q = 0; q < CM; ++q) g[q] = g2s[rl][q];
     float* g1row = G1 + (int64_t)rowc * hidden;
 #pragma unroll
     for (int k = 0; k < NH; ++k) {
@@ -381,10 +436,9 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
         const float* w = w2s + j * LR;
         float v = 0.0f;
 #pragma unroll
-        for (int c = 0; c < CM; ++c) v = fmaf(g[c], w[c], v);
+        for (int q = 0; q < CM; ++q) v = fmaf(g[q], w[q], v);
         if (live && j < hidden) g1row[j] = h[k] > 0.0f ? v : 0.0f;
     }
-    __syncthreads();
     if (t <= classes) {
 #pragma clang fp contract(off)
         float acc = 0.0f;
