@@ -204,7 +204,9 @@ def gemm_case(capi, torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1
     """Resident operands and a launcher closure for one GEMM configuration.
 
     rotate > 1 cycles through that many copies of the operands so the working
-    set exceeds the 256 MB Infinity Cache (HBM-bound shapes).
+    set exceeds the 256 MB Infinity Cache (HBM-bound shapes).  The call is the
+    one the dl:: operations make: fdl_sgemm_ex_ws with the workspace
+    fdl_sgemm_workspace_size asks for when it asks for one, else fdl_sgemm_ex.
     """
     gen = torch.Generator(device="cuda").manual_seed(seed)
     a_shape = (batch, K, M) if ta else (batch, M, K)
@@ -217,13 +219,19 @@ def gemm_case(capi, torch, M, N, K, ta=0, tb=0, batch=1, epi=0, seed=0, rotate=1
     ldb = K if tb else N
     stream = torch.cuda.current_stream().cuda_stream
     state = {"i": 0}
+    ws_bytes = capi.workspace_size(ta, tb, M, N, K, batch)
+    ws = torch.empty((ws_bytes // 4,), device="cuda") if ws_bytes else None
 
     def launch():
         i = state["i"]
         state["i"] = (i + 1) % rotate
-        capi.sgemm_ex(ta, tb, M, N, K, As[i].data_ptr(), lda, M * K, Bs[i].data_ptr(), ldb,
-                      K * N, Cs[i].data_ptr(), N, M * N, batch,
-                      bias.data_ptr() if epi in (1, 2) else None, None, epi, stream)
+        args = (ta, tb, M, N, K, As[i].data_ptr(), lda, M * K, Bs[i].data_ptr(), ldb, K * N,
+                Cs[i].data_ptr(), N, M * N, batch, bias.data_ptr() if epi in (1, 2) else None,
+                None, epi)
+        if ws is None:
+            capi.sgemm_ex(*args, stream)
+        else:
+            capi.sgemm_ex_ws(*args, ws.data_ptr(), ws_bytes, stream)
 
     return launch, As[0], Bs[0], Cs[0]
 

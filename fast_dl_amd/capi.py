@@ -39,6 +39,10 @@ SIGNATURES = {
     "fdl_sgemm_ex_select": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                    _i64, _vp, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp]),
     "fdl_sgemm_kernel_choice": (_int, [_int, _int, _i64, _i64, _i64, _i64]),
+    "fdl_sgemm_workspace_size": (ctypes.c_size_t, [_int, _int, _i64, _i64, _i64, _i64]),
+    "fdl_sgemm_ex_ws": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                               _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, ctypes.c_size_t,
+                               _vp]),
     "fdl_gemm": (_int, [_vp, _vp, _vp, _int, _int, _int]),
     "fdl_add_row_bias": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "fdl_relu": (_int, [_vp, _vp, _i64, _vp]),
@@ -105,6 +109,7 @@ def _checked(name: str):
 
 sgemm_ex = _checked("fdl_sgemm_ex")
 sgemm_ex_select = _checked("fdl_sgemm_ex_select")
+sgemm_ex_ws = _checked("fdl_sgemm_ex_ws")
 gemm = _checked("fdl_gemm")
 add_row_bias = _checked("fdl_add_row_bias")
 relu = _checked("fdl_relu")
@@ -135,6 +140,11 @@ def mlp2_graph_create(*args) -> int:
 
 def kernel_choice(transA: int, transB: int, M: int, N: int, K: int, batch: int = 1) -> int:
     return load_library().fdl_sgemm_kernel_choice(transA, transB, M, N, K, batch)
+
+
+def workspace_size(transA: int, transB: int, M: int, N: int, K: int, batch: int = 1) -> int:
+    """Bytes of workspace fdl_sgemm_ex_ws can use for this problem (0: none)."""
+    return load_library().fdl_sgemm_workspace_size(transA, transB, M, N, K, batch)
 
 
 def version() -> str:

@@ -7,6 +7,7 @@
 #include "../../include/fastdl_gemm.h"
 
 #include <climits>
+#include <cstdint>
 #include <cmath>
 #include <cstdio>
 #include <string>
@@ -31,13 +32,14 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
-                        const float* A, int64_t lda, int64_t strideA, const float* B,
-                        int64_t ldb, int64_t strideB, float* C, int64_t ldc,
-                        int64_t strideC, int64_t batch, const float* bias,
-                        const float* aux, int epilogue, int kernel, void* stream) {
+// fdl_sgemm_ex_select with an optional workspace (fdl_sgemm_ex_ws).
+int sgemm_impl(int transA, int transB, int64_t M, int64_t N, int64_t K, const float* A,
+               int64_t lda, int64_t strideA, const float* B, int64_t ldb, int64_t strideB,
+               float* C, int64_t ldc, int64_t strideC, int64_t batch, const float* bias,
+               const float* aux, int epilogue, int kernel, void* workspace,
+               size_t workspace_bytes, void* stream) {
     if (kernel < FDL_KERNEL_AUTO || kernel > FDL_KERNEL_DMA96X32U) {
         return fail(FDL_ERROR_INVALID_VALUE, "sgemm: unknown kernel family");
     }
@@ -112,8 +114,47 @@ int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
                     "sgemm: the 4-byte direct-to-LDS kernels need leading dimensions up to 2^24 "
                     "and 4-byte-aligned operands");
     }
-    return check_hip(fdl::launch_sgemm(p, ta, tb, batch, kern, as_stream(stream)),
+    if (workspace != nullptr && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) {
+        return fail(FDL_ERROR_INVALID_VALUE, "sgemm: workspace must be 16-byte aligned");
+    }
+    return check_hip(fdl::launch_sgemm(p, ta, tb, batch, kern, as_stream(stream),
+                                       static_cast<float*>(workspace),
+                                       workspace ? workspace_bytes : 0),
                      "sgemm launch failed");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdl_sgemm_ex_select(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                        const float* A, int64_t lda, int64_t strideA, const float* B,
+                        int64_t ldb, int64_t strideB, float* C, int64_t ldc,
+                        int64_t strideC, int64_t batch, const float* bias,
+                        const float* aux, int epilogue, int kernel, void* stream) {
+    return sgemm_impl(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
+                      strideC, batch, bias, aux, epilogue, kernel, nullptr, 0, stream);
+}
+
+int fdl_sgemm_ex_ws(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                    const float* A, int64_t lda, int64_t strideA, const float* B,
+                    int64_t ldb, int64_t strideB, float* C, int64_t ldc,
+                    int64_t strideC, int64_t batch, const float* bias,
+                    const float* aux, int epilogue, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    return sgemm_impl(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
+                      strideC, batch, bias, aux, epilogue, FDL_KERNEL_AUTO, workspace,
+                      workspace_bytes, stream);
+}
+
+size_t fdl_sgemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                                int64_t batch) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K) || batch < 1) return 0;
+    fdl::GemmParams p{};
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    return fdl::skinny_split_plan(p, transA == FDL_OP_T, transB == FDL_OP_T, batch).bytes;
 }
 
 int fdl_sgemm_ex(int transA, int transB, int64_t M, int64_t N, int64_t K,

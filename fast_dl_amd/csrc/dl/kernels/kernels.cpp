@@ -2,14 +2,43 @@
 // Each maps one reference launcher (include/dl/kernels/*.hpp of the
 // reference) onto this build's gfx950 kernels and turns a non-zero status
 // into std::runtime_error.
+#include "sgemm_call.hpp"
+#include "../tensor/block_cache.hpp"
+
 #include <dl/core/HipUtils.hpp>
 #include <dl/core/Stream.hpp>
 #include <dl/kernels/kernels.hpp>
 
 #include <fastdl_gemm.h>
 
+#include <hip/hip_runtime_api.h>
+
 #include <stdexcept>
 #include <string>
+
+namespace dl::detail {
+
+int sgemm_auto(int transA, int transB, int64_t M, int64_t N, int64_t K, const float* A,
+               int64_t lda, int64_t strideA, const float* B, int64_t ldb, int64_t strideB,
+               float* C, int64_t ldc, int64_t strideC, int64_t batch, const float* bias,
+               const float* aux, int epilogue, void* stream) {
+    const size_t bytes = fdl_sgemm_workspace_size(transA, transB, M, N, K, batch);
+    if (bytes == 0) {
+        return fdl_sgemm_ex(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
+                            strideC, batch, bias, aux, epilogue, stream);
+    }
+    int device = 0;
+    hip::check(hipGetDevice(&device), "cudaGetDevice failed");
+    BlockCache& cache = device_block_cache();
+    void* ws = cache.acquire(device, bytes, stream);
+    const int status = fdl_sgemm_ex_ws(transA, transB, M, N, K, A, lda, strideA, B, ldb,
+                                       strideB, C, ldc, strideC, batch, bias, aux, epilogue, ws,
+                                       bytes, stream);
+    cache.release(device, bytes, ws, stream, {});
+    return status;
+}
+
+}  // namespace dl::detail
 
 namespace dl::kernels {
 
@@ -76,12 +105,19 @@ void gemm_ex(Transpose trans_a, Transpose trans_b, int64_t m, int64_t n, int64_t
              int64_t stride_b, float* c, int64_t ldc, int64_t stride_c, int64_t batch,
              const float* bias, const float* aux, Epilogue epilogue, GemmAlgo algo,
              void* stream) {
-    hip::check_fdl(
-        fdl_sgemm_ex_select(trans_a == Transpose::Yes ? FDL_OP_T : FDL_OP_N,
-                            trans_b == Transpose::Yes ? FDL_OP_T : FDL_OP_N, m, n, k, a, lda,
-                            stride_a, b, ldb, stride_b, c, ldc, stride_c, batch, bias, aux,
-                            epilogue_id(epilogue), kernel_id(algo), stream),
-        "gemm failed");
+    const int ta = trans_a == Transpose::Yes ? FDL_OP_T : FDL_OP_N;
+    const int tb = trans_b == Transpose::Yes ? FDL_OP_T : FDL_OP_N;
+    if (algo == GemmAlgo::Auto) {
+        hip::check_fdl(detail::sgemm_auto(ta, tb, m, n, k, a, lda, stride_a, b, ldb, stride_b, c,
+                                          ldc, stride_c, batch, bias, aux, epilogue_id(epilogue),
+                                          stream),
+                       "gemm failed");
+        return;
+    }
+    hip::check_fdl(fdl_sgemm_ex_select(ta, tb, m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc,
+                                       stride_c, batch, bias, aux, epilogue_id(epilogue),
+                                       kernel_id(algo), stream),
+                   "gemm failed");
 }
 
 void add_row_bias(float* output, const float* bias, int rows, int cols) {

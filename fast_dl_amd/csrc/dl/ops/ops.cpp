@@ -5,6 +5,7 @@
 // second pass over the output.  matmul, linear, linear_relu, relu and
 // cross_entropy record their backward node when an input requires a gradient.
 #include "../autograd/record.hpp"
+#include "../kernels/sgemm_call.hpp"
 
 #include <dl/core/HipUtils.hpp>
 #include <dl/core/Stream.hpp>
@@ -108,7 +109,7 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
     const int64_t m = a.shape()[0], k = a.shape()[1], n = b.shape()[1];
     Tensor out(Shape({m, n}), a.dtype(), a.device());
     set_device(a);
-    hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, m, n, k, f32(a), k, 0, f32(b), n, 0,
+    hip::check_fdl(detail::sgemm_auto(FDL_OP_N, FDL_OP_N, m, n, k, f32(a), k, 0, f32(b), n, 0,
                                 f32(out), n, 0, 1, nullptr, nullptr, FDL_EPILOGUE_NONE, current_stream()),
                    "matmul kernel launch failed");
     if (autograd::any_requires_grad({&a, &b})) {
@@ -150,7 +151,7 @@ Tensor linear_impl(const Tensor& input, const Tensor& weight, const Tensor& bias
     const int64_t rows = input.shape()[0], in = input.shape()[1], out_f = weight.shape()[1];
     Tensor out(Shape({rows, out_f}), input.dtype(), input.device());
     set_device(input);
-    hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_N, rows, out_f, in, f32(input), in, 0,
+    hip::check_fdl(detail::sgemm_auto(FDL_OP_N, FDL_OP_N, rows, out_f, in, f32(input), in, 0,
                                 f32(weight), out_f, 0, f32(out), out_f, 0, 1, f32(bias), nullptr,
                                 epilogue, current_stream()),
                    "linear kernel launch failed");
@@ -200,14 +201,14 @@ LinearGrads linear_backward(const Tensor& grad_output, const Tensor& input, cons
     if (need_grad_input) {
         g.grad_input = Tensor(Shape({rows, in}), DType::Float32, input.device());
         // dX = dY W^T  (NT)
-        hip::check_fdl(fdl_sgemm_ex(FDL_OP_N, FDL_OP_T, rows, in, out_f, f32(grad_output), out_f, 0,
+        hip::check_fdl(detail::sgemm_auto(FDL_OP_N, FDL_OP_T, rows, in, out_f, f32(grad_output), out_f, 0,
                                     f32(weight), out_f, 0, f32(g.grad_input), in, 0, 1, nullptr,
                                     nullptr, FDL_EPILOGUE_NONE, current_stream()),
                        "linear_backward grad_input failed");
     }
     // dW = X^T dY  (TN)
     g.grad_weight = Tensor(Shape({in, out_f}), DType::Float32, input.device());
-    hip::check_fdl(fdl_sgemm_ex(FDL_OP_T, FDL_OP_N, in, out_f, rows, f32(input), in, 0,
+    hip::check_fdl(detail::sgemm_auto(FDL_OP_T, FDL_OP_N, in, out_f, rows, f32(input), in, 0,
                                 f32(grad_output), out_f, 0, f32(g.grad_weight), out_f, 0, 1,
                                 nullptr, nullptr, FDL_EPILOGUE_NONE, current_stream()),
                    "linear_backward grad_weight failed");

@@ -96,9 +96,27 @@ inline hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStrea
     return launch_group(jobs, 2, stream);
 }
 
+// K-split form of the skinny family (sgemm.hip): B's columns in bands of
+// kSplitBand, K in `slices` slices of `rows` rows, one block per (band,
+// slice) writing an mr x kSplitBand partial, then a pass adding the slices.
+// slices == 0: the problem does not take the split (not one skinny problem
+// with B not transposed and N % 4 == 0, or too little of B to pay for the
+// second pass).
+constexpr int kSplitBand = 256;
+constexpr int kSplitMaxSlices = 64;
+struct SkinnySplit {
+    int mr = 0, bands = 0, slices = 0, rows = 0;
+    size_t bytes = 0;  // workspace the partials take
+};
+SkinnySplit skinny_split_plan(const GemmParams& p, bool transA, bool transB, int64_t batch);
+
 // Launches `batch` problems (grid.y indexes the batch).  Returns a hipError_t.
+// With a workspace of at least skinny_split_plan(...).bytes, a problem the
+// skinny family runs takes the K-split form (when B is 16-byte
+// vectorisable); the workspace is written on `stream`.
 hipError_t launch_sgemm(const GemmParams& p, bool transA, bool transB,
-                        int64_t batch, GemmKernel kernel, hipStream_t stream);
+                        int64_t batch, GemmKernel kernel, hipStream_t stream,
+                        float* workspace = nullptr, size_t workspace_bytes = 0);
 
 // Kernel the dispatcher would pick for this problem.
 GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,

@@ -1500,6 +1500,127 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
 }
 
 // ---------------------------------------------------------------------------
+// K-split form of the skinny kernel, run when the caller supplies a workspace
+// (one problem, B not transposed, 16-byte-vectorisable B).  When B's row
+// pitch is a power of two (N = 4096: 16 KB) the strip kernel's blocks, each
+// held to one 64-byte column piece of every row, stream at uneven rates: the
+// pieces at some offsets within each 1 KB of a row are served much more
+// slowly than the rest, so a few blocks finish long after the median.  Here a
+// block owns a band of 256 columns (1 KB of each row, every offset) and a
+// slice of K, so every block sees the same mix of offsets.  The price is a
+// second, small pass.
+//
+// Pass 1 (skinny_part): block (band, slice) streams rows [k0, k1) of its band
+// with four waves, each wave reading whole 1 KB row pieces (a lane a float4)
+// with UNR rows in flight, the wave's rows interleaved by 4.  The four waves'
+// sums meet in LDS, added in wave order, and the block writes its MR x 256
+// partial to part[band][slice] in the workspace.
+// Pass 2 (skinny_sum): one thread per output element adds its band's slices
+// in slice order and applies the epilogue.  Both orders are fixed, so results
+// repeat bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int kSplitWaves = 4;
+constexpr int64_t kSplitMinElems = int64_t(1) << 23;   // 32 MB of B
+
+template <int MR, bool TA, int UNR>
+__global__ void __launch_bounds__(kSplitWaves * kWave)
+sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part) {
+    constexpr int NW = kSplitWaves;
+    __shared__ float red[NW][MR][kSplitBand];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    // wave-uniform, so A's loads below have wave-uniform addresses
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+
+    const int tiles = gridDim.x;
+    int t = blockIdx.x;
+    // each XCD takes a contiguous range of (band, slice) tiles: whole bands
+    if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+    const int band = t / S;
+    const int slice = t - band * S;
+    const int k0 = slice * rows;
+    const int k1 = min(k0 + rows, p.K);
+    // N % 4 == 0 here; lanes past the edge re-read the last float4 and their
+    // sums land only in partial slots that pass 2 never reads.
+    const int n0 = min(band * kSplitBand + lane * 4, p.N - 4);
+    const float* __restrict__ A = p.A;
+    const float* __restrict__ B = p.B;
+    const int M = p.M;
+
+    float acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
+    auto a_at = [&](int m, int k) {
+        const int mm = min(m, M - 1);
+        return TA ? A[(int64_t)k * p.lda + mm] : A[(int64_t)mm * p.lda + k];
+    };
+
+    int k = k0 + w;
+    for (; k + NW * (UNR - 1) < k1; k += NW * UNR) {
+        floatx4 b[UNR];
+        float a[UNR][MR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+            b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(k + NW * u) * p.ldb + n0);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) a[u][m] = a_at(m, k + NW * u);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(a[u][m], b[u][c], acc[m][c]);
+    }
+    for (; k < k1; k += NW) {
+        const floatx4 b = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + n0);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float a = a_at(m, k);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(a, b[c], acc[m][c]);
+        }
+    }
+
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[w][m][lane * 4 + c] = acc[m][c];
+    __syncthreads();
+    float* __restrict__ mine = part + (int64_t)t * MR * kSplitBand;
+    for (int e = tid; e < MR * kSplitBand; e += NW * kWave) {
+        const int m = e / kSplitBand;
+        const int c = e % kSplitBand;
+        float v = red[0][m][c];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) v += red[q][m][c];
+        mine[e] = v;
+    }
+}
+
+// All SMAX loads are issued before the first add (slices past S re-read the
+// last one and are not added), so the pass costs one memory round trip.
+template <int MR, int SMAX>
+__global__ void __launch_bounds__(kSplitBand)
+sgemm_skinny_sum_kernel(GemmParams p, int S, const float* __restrict__ part) {
+    const int band = blockIdx.x;
+    const int m = blockIdx.y;
+    const int j = band * kSplitBand + (int)threadIdx.x;
+    if (j >= p.N) return;
+    const float* __restrict__ src = part + ((int64_t)band * S * MR + m) * kSplitBand + threadIdx.x;
+    float x[SMAX];
+#pragma unroll
+    for (int u = 0; u < SMAX; ++u) x[u] = src[(int64_t)min(u, S - 1) * MR * kSplitBand];
+    float v = 0.0f;
+#pragma unroll
+    for (int u = 0; u < SMAX; ++u) v += u < S ? x[u] : 0.0f;
+    store_epilogue(v, p, p.C, p.aux, p.upd, (int64_t)m * p.ldc + j, j);
+}
+
+// ---------------------------------------------------------------------------
 // Host-side launchers.
 // ---------------------------------------------------------------------------
 
@@ -1778,6 +1899,45 @@ hipError_t launch_skinny(const GemmParams& p, bool ta, bool vb, int nbatch,
     return launch_skinny_mr<8>(p, ta, vb, nbatch, stream);
 }
 
+template <int MR>
+hipError_t launch_skinny_split_mr(const GemmParams& p, bool ta, const SkinnySplit& s,
+                                  float* part, hipStream_t stream) {
+    constexpr int UNR = 4;
+    const dim3 grid1(s.bands * s.slices);
+    const dim3 block1(kSplitWaves * kWave);
+    if (ta) {
+        hipLaunchKernelGGL((sgemm_skinny_part_kernel<MR, true, UNR>), grid1, block1, 0, stream,
+                           p, s.slices, s.rows, part);
+    } else {
+        hipLaunchKernelGGL((sgemm_skinny_part_kernel<MR, false, UNR>), grid1, block1, 0, stream,
+                           p, s.slices, s.rows, part);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const dim3 grid2(s.bands, p.M);
+    if (s.slices <= 16) {
+        hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, 16>), grid2, dim3(kSplitBand), 0, stream,
+                           p, s.slices, part);
+    } else if (s.slices <= 32) {
+        hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, 32>), grid2, dim3(kSplitBand), 0, stream,
+                           p, s.slices, part);
+    } else {
+        hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, kSplitMaxSlices>), grid2,
+                           dim3(kSplitBand), 0, stream, p, s.slices, part);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_skinny_split(const GemmParams& p, bool ta, const SkinnySplit& s,
+                               float* part, hipStream_t stream) {
+    switch (s.mr) {
+        case 1: return launch_skinny_split_mr<1>(p, ta, s, part, stream);
+        case 2: return launch_skinny_split_mr<2>(p, ta, s, part, stream);
+        case 4: return launch_skinny_split_mr<4>(p, ta, s, part, stream);
+        default: return launch_skinny_split_mr<8>(p, ta, s, part, stream);
+    }
+}
+
 constexpr int kMaxGridY = 65535;
 
 // Production tile configurations (BM, BN, BK, WM, WN, PAD, waves per SIMD).
@@ -1976,6 +2136,31 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
     return best;
 }
 
+SkinnySplit skinny_split_plan(const GemmParams& p, bool transA, bool transB, int64_t batch) {
+    SkinnySplit s;
+    if (batch != 1 || choose_kernel(p, transA, transB, batch) != GemmKernel::Skinny) return s;
+    if (p.M < 1 || p.N % 4 != 0 || p.K < 1) return s;
+    // The second pass costs about 3 us.  It pays when each strip of the
+    // single pass is long (K >= 4096: 1.1x at N = 4096, 1.35x at N = 1024,
+    // 3.2x at N = 1024, K = 16384) or B is large (N = 16384, K = 1024:
+    // 1.2x), not for shorter K at moderate size (N = 4096, K = 1024: 0.75x;
+    // N = 1024, K = 2048: 0.94x).
+    if (p.K < 4096 && (int64_t)p.N * p.K < kSplitMinElems) return s;
+    // About two rounds of the 256 CUs, slices of at least 64 rows.
+    const int64_t bands = (p.N + kSplitBand - 1) / kSplitBand;
+    int64_t slices = std::min<int64_t>(kSplitMaxSlices, (512 + bands - 1) / bands);
+    int64_t rows = (p.K + slices - 1) / slices;
+    rows = std::max<int64_t>(64, (rows + 7) / 8 * 8);
+    slices = (p.K + rows - 1) / rows;
+    if (slices < 2 || bands * slices > (1 << 22)) return s;
+    s.mr = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : 8;
+    s.bands = (int)bands;
+    s.slices = (int)slices;
+    s.rows = (int)rows;
+    s.bytes = (size_t)bands * slices * s.mr * kSplitBand * sizeof(float);
+    return s;
+}
+
 namespace {
 
 GroupDev group_dev(const GroupJob& j) {
@@ -2072,7 +2257,8 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
 }
 
 hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
-                        int64_t batch, GemmKernel kernel, hipStream_t stream) {
+                        int64_t batch, GemmKernel kernel, hipStream_t stream,
+                        float* workspace, size_t workspace_bytes) {
     if (batch <= 0 || p0.M <= 0 || p0.N <= 0) return hipSuccess;
     const bool automatic = kernel == GemmKernel::Auto;
     if (automatic) kernel = choose_kernel(p0, transA, transB, batch);
@@ -2127,9 +2313,16 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
             case GemmKernel::SplitK16:
                 err = launch_splitk16(p, transA, transB, va, vb, nb, stream);
                 break;
-            case GemmKernel::Skinny:
-                err = launch_skinny(p, transA, vb, nb, stream);
+            case GemmKernel::Skinny: {
+                const SkinnySplit split = skinny_split_plan(p0, transA, transB, batch);
+                if (workspace != nullptr && split.slices > 0 && vb &&
+                    workspace_bytes >= split.bytes) {
+                    err = launch_skinny_split(p, transA, split, workspace, stream);
+                } else {
+                    err = launch_skinny(p, transA, vb, nb, stream);
+                }
                 break;
+            }
             case GemmKernel::Dma256:
                 err = launch_dma<CfgDma256>(p, transA, transB, nb, stream);
                 break;

@@ -315,9 +315,16 @@ def write_traces(d: str) -> dict:
             L.append(f"{len(ts):6d} {sum(ts) / len(ts):9.2f} {min(ts):9.2f} "
                      f"{timed_mean(ts, w.steps):9.2f}  {short(n)[:140]}")
         if w.kind == "gemm":
-            name, t, _ = _dominant(tr, w.steps)
+            name, t, calls = _dominant(tr, w.steps)
+            # a call of two launches (the skinny K split: partials, then their
+            # sum) counts both
+            group = [n for n, ts in agg.items() if len(ts) == calls]
+            fam = kernel_family(name)
+            if len(group) > 1:
+                t = sum(timed_mean(agg[n], w.steps) for n in group)
+                fam = " + ".join(kernel_family(n) for n in group)
             fl, by = flops_bytes(cfg)
-            L.append(f"  => {kernel_family(name)} {t:.2f} us: {fl / t / 1e6:.2f} TFLOP/s "
+            L.append(f"  => {fam} {t:.2f} us: {fl / t / 1e6:.2f} TFLOP/s "
                      f"({100 * fl / t / 1e6 / PEAK_TFLOPS:.1f}% of {PEAK_TFLOPS}), "
                      f"{by / t / 1e3:.0f} GB/s ({100 * by / t / 1e3 / PEAK_GBS:.1f}% of 8 TB/s)")
             out[cfg] = (name, t)

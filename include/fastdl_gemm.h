@@ -30,6 +30,7 @@
 #ifndef FASTDL_GEMM_H
 #define FASTDL_GEMM_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -135,6 +136,39 @@ int fdl_sgemm_ex_select(int transA, int transB,
 /* Kernel family fdl_sgemm_ex would use for this problem (FDL_KERNEL_*). */
 int fdl_sgemm_kernel_choice(int transA, int transB,
                             int64_t M, int64_t N, int64_t K, int64_t batch);
+
+/*
+ * Workspace, in bytes, that fdl_sgemm_ex_ws can use for this problem; 0 when
+ * it would use none.  Non-zero only for one problem (batch == 1) that the
+ * skinny family runs (M <= 8, transB == N) with N % 4 == 0 and enough work
+ * to pay for a second pass (K >= 4096, or N * K >= 2^23).  This build's own extension: the
+ * reference called cublasSgemm, which takes no workspace
+ * (src/kernels/cuda/gemm.cu:166-177).
+ */
+size_t fdl_sgemm_workspace_size(int transA, int transB,
+                                int64_t M, int64_t N, int64_t K, int64_t batch);
+
+/*
+ * fdl_sgemm_ex with a caller-owned device workspace (16-byte aligned, or
+ * NULL).  Given at least fdl_sgemm_workspace_size() bytes, and B 16-byte
+ * vectorisable, a skinny problem splits K over blocks: each block streams a
+ * 256-column band of B over one slice of K and writes partial sums to the
+ * workspace, and a second launch adds the slices in slice order and applies
+ * the epilogue.  Results repeat bit for bit, and differ from fdl_sgemm_ex's
+ * single pass only in the order of the fp32 additions.  Every other problem,
+ * or a smaller workspace, runs exactly as fdl_sgemm_ex.  The workspace is
+ * written on `stream`: work on other streams must not use it until the call's
+ * work there has finished.
+ */
+int fdl_sgemm_ex_ws(int transA, int transB,
+                    int64_t M, int64_t N, int64_t K,
+                    const float* A, int64_t lda, int64_t strideA,
+                    const float* B, int64_t ldb, int64_t strideB,
+                    float* C, int64_t ldc, int64_t strideC,
+                    int64_t batch,
+                    const float* bias, const float* aux, int epilogue,
+                    void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 /*
  * C[m,n] = A[m,k] . B[k,n], row-major, contiguous, null stream.

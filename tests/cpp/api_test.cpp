@@ -119,6 +119,29 @@ int main() {
         return yr[0] == 0.0f && yr[2] == 0.0f && std::fabs(yr[1] - 29.0f) < 1e-4f;
     });
 
+    run("matmul_skinny_k_split", [] {
+        // 3 x 4096 times 4096 x 1024: the skinny family's K-split form, its
+        // partials in a workspace from the block cache.  Repeated calls on the
+        // null stream and on a user stream (each reusing the cached
+        // workspace) give the same bits.
+        const int m = 3, k = 4096, n = 1024;
+        auto a = randv(m * k, 21), b = randv(k * n, 22);
+        auto want = host_gemm(a, b, m, n, k);
+        auto ta = dl::Tensor::from_host<float>(a, dl::Shape({m, k}), kDev);
+        auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
+        const auto first = dl::ops::matmul(ta, tb).to_host<float>();
+        bool ok = close(first, want, 1e-5f) && dl::ops::matmul(ta, tb).to_host<float>() == first;
+        dl::Stream s(kDev);
+        {
+            dl::StreamGuard g(s);
+            auto c1 = dl::ops::matmul(ta, tb);
+            auto c2 = dl::ops::matmul(ta, tb);
+            dl::synchronize();
+            ok = ok && c1.to_host<float>() == first && c2.to_host<float>() == first;
+        }
+        return ok;
+    });
+
     run("matmul_random_all_algos", [] {
         const int m = 100, n = 70, k = 50;
         auto a = randv(m * k, 1), b = randv(k * n, 2);

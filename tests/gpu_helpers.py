@@ -49,10 +49,12 @@ def operands(g: np.random.Generator, ta, tb, M, N, K, batch, dist="normal", scal
 
 
 def gpu_sgemm(ta, tb, A, B, M, N, K, batch=1, bias=None, aux=None, epilogue=0,
-              kernel=capi.KERNEL_AUTO, lda=None, ldb=None, ldc=None):
+              kernel=capi.KERNEL_AUTO, lda=None, ldb=None, ldc=None, workspace=None):
     """Run fdl_sgemm_ex_select on packed operands; returns C [batch, M, N] on the host.
 
     C is pre-filled with NaN so an element the kernel fails to write is caught.
+    With ``workspace`` (a byte count) the call is fdl_sgemm_ex_ws with a
+    NaN-filled workspace of that size instead.
     """
     import torch
 
@@ -74,11 +76,18 @@ def gpu_sgemm(ta, tb, A, B, M, N, K, batch=1, bias=None, aux=None, epilogue=0,
         aux_p = np.zeros((batch, M, ldc), np.float32)
         aux_p[:, :, :N] = aux.reshape(batch, M, N)
         daux = dev(aux_p)
-    capi.sgemm_ex_select(ta, tb, M, N, K, dA.data_ptr(), lda, sA, dB.data_ptr(), ldb, sB,
-                         dC.data_ptr(), ldc, sC, batch,
-                         dbias.data_ptr() if dbias is not None else None,
-                         daux.data_ptr() if daux is not None else None,
-                         epilogue, kernel, stream())
+    ptrs = (dbias.data_ptr() if dbias is not None else None,
+            daux.data_ptr() if daux is not None else None)
+    if workspace is None:
+        capi.sgemm_ex_select(ta, tb, M, N, K, dA.data_ptr(), lda, sA, dB.data_ptr(), ldb, sB,
+                             dC.data_ptr(), ldc, sC, batch, *ptrs, epilogue, kernel, stream())
+    else:
+        assert kernel == capi.KERNEL_AUTO
+        ws = torch.full((max(1, workspace // 4),), float("nan"), dtype=torch.float32,
+                        device="cuda")
+        capi.sgemm_ex_ws(ta, tb, M, N, K, dA.data_ptr(), lda, sA, dB.data_ptr(), ldb, sB,
+                         dC.data_ptr(), ldc, sC, batch, *ptrs, epilogue, ws.data_ptr(),
+                         workspace, stream())
     return host(dC)[:, :, :N]
 
 

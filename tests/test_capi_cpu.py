@@ -159,3 +159,26 @@ def test_idx_gather_argument_validation():
         assert capi.last_error().startswith("idx_gather:")
     # no-ops and inputs that may be null: nothing is launched
     assert _gather_status(batch=0, images=None, labels=None, x=None, y=None) == 0
+
+
+def test_workspace_size():
+    # the skinny family's K split: 256-column bands x K slices x M rows rounded
+    # up to 1, 2, 4 or 8, in floats
+    assert capi.workspace_size(0, 0, 1, 4096, 4096) == 16 * 32 * 1 * 256 * 4
+    assert capi.workspace_size(0, 0, 8, 4096, 4096) == 16 * 32 * 8 * 256 * 4
+    assert capi.workspace_size(1, 0, 3, 4096, 4096) == 16 * 32 * 4 * 256 * 4
+    assert capi.workspace_size(0, 0, 1, 1024, 16384) == 4 * 64 * 256 * 4
+    assert capi.workspace_size(0, 0, 8, 16384, 1024) > 0     # 64 MB of B
+    assert capi.workspace_size(0, 0, 4, 4096, 1024) == 0     # 16 MB, short K: single pass
+    assert capi.workspace_size(0, 1, 1, 4096, 4096) == 0     # B transposed
+    assert capi.workspace_size(0, 0, 1, 4096, 4096, 2) == 0  # batched
+    assert capi.workspace_size(0, 0, 9, 4096, 4096) == 0     # not skinny
+    assert capi.workspace_size(0, 0, 1, 4098, 4096) == 0     # N % 4 != 0
+    assert capi.workspace_size(0, 0, 1, 4096, 4096, 0) == 0
+
+
+def test_workspace_validation():
+    args = [0, 0, 1, 4096, 4096, 1 << 20, 4096, 0, 1 << 20, 4096, 0, 1 << 20, 4096, 0, 1,
+            None, None, 0]
+    assert capi.raw_call("fdl_sgemm_ex_ws", *args, (1 << 20) + 4, 1 << 20, None) == -1
+    assert "16-byte aligned" in capi.last_error()
