@@ -40,6 +40,8 @@ SIGNATURES = {
                                    _i64, _vp, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp]),
     "fdl_sgemm_kernel_choice": (_int, [_int, _int, _i64, _i64, _i64, _i64]),
     "fdl_sgemm_workspace_size": (ctypes.c_size_t, [_int, _int, _i64, _i64, _i64, _i64]),
+    "fdl_sgemm_ex_noalloc": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                                    _i64, _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "fdl_sgemm_ex_ws": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, ctypes.c_size_t,
                                _vp]),
@@ -110,6 +112,7 @@ def _checked(name: str):
 sgemm_ex = _checked("fdl_sgemm_ex")
 sgemm_ex_select = _checked("fdl_sgemm_ex_select")
 sgemm_ex_ws = _checked("fdl_sgemm_ex_ws")
+sgemm_ex_noalloc = _checked("fdl_sgemm_ex_noalloc")
 gemm = _checked("fdl_gemm")
 add_row_bias = _checked("fdl_add_row_bias")
 relu = _checked("fdl_relu")

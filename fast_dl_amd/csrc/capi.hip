@@ -1,6 +1,7 @@
 // extern "C" entry points declared in include/fastdl_gemm.h: argument
 // validation, status codes and dispatch onto the kernels.  Nothing here
-// allocates memory or synchronises the stream.
+// allocates memory or synchronises the stream.  fdl_sgemm_ex_noalloc's scratch
+// is a static device array (one per GPU, for the life of the process).
 #include "fdl_internal.hpp"
 
 #include "../../include/fastdl_data.h"
@@ -10,6 +11,7 @@
 #include <cstdint>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -123,6 +125,43 @@ int sgemm_impl(int transA, int transB, int64_t M, int64_t N, int64_t K, const fl
                      "sgemm launch failed");
 }
 
+// Scratch of fdl_sgemm_ex_noalloc: the partial sums of the skinny family's
+// K split (at most 4 MiB: M <= 8, N = K = 4096).  Each GPU holds its own copy
+// at its own address; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices] = {};
+
+// The current device's scratch address, looked up (with that device
+// current) on the first call on the device.  Returns an fdl status.
+int device_scratch(float** out) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) {
+        return fail(FDL_ERROR_RUNTIME,
+                    std::string("sgemm_noalloc: hipGetDevice: ") + hipGetErrorString(err));
+    }
+    if (device < 0 || device >= kScratchDevices) {
+        return fail(FDL_ERROR_NOT_SUPPORTED, "sgemm_noalloc: device index beyond the scratch table");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || ptr == nullptr) {
+            return fail(FDL_ERROR_RUNTIME, std::string("sgemm_noalloc: hipGetSymbolAddress: ") +
+                                               hipGetErrorString(err));
+        }
+        g_scratch_ptr[device] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch_ptr[device];
+    return FDL_SUCCESS;
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,6 +184,28 @@ int fdl_sgemm_ex_ws(int transA, int transB, int64_t M, int64_t N, int64_t K,
     return sgemm_impl(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
                       strideC, batch, bias, aux, epilogue, FDL_KERNEL_AUTO, workspace,
                       workspace_bytes, stream);
+}
+
+int fdl_sgemm_ex_noalloc(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                         const float* A, int64_t lda, int64_t strideA, const float* B,
+                         int64_t ldb, int64_t strideB, float* C, int64_t ldc,
+                         int64_t strideC, int64_t batch, const float* bias,
+                         const float* aux, int epilogue, void* stream) {
+    const size_t need = fdl_sgemm_workspace_size(transA, transB, M, N, K, batch);
+    if (need > kScratchBytes) {
+        return fail(FDL_ERROR_INVALID_VALUE,
+                    "sgemm_noalloc: the problem needs " + std::to_string(need) +
+                        " bytes of scratch, more than the " + std::to_string(kScratchBytes) +
+                        " the library holds per device");
+    }
+    float* ws = nullptr;
+    if (need > 0 && M > 0 && N > 0) {
+        const int status = device_scratch(&ws);
+        if (status != FDL_SUCCESS) return status;
+    }
+    return sgemm_impl(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
+                      strideC, batch, bias, aux, epilogue, FDL_KERNEL_AUTO, ws,
+                      ws ? kScratchBytes : 0, stream);
 }
 
 size_t fdl_sgemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int64_t K,

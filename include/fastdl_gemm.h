@@ -171,6 +171,28 @@ int fdl_sgemm_ex_ws(int transA, int transB,
                     void* stream);
 
 /*
+ * fdl_sgemm_ex_ws with the library's own scratch in place of a workspace
+ * argument: allocates nothing (no hipMalloc, no hipFree, no allocating
+ * library call), for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  It has no
+ * counterpart in the reference.  The scratch is a static device array of
+ * 4 MiB per GPU, held until the process ends; a problem whose
+ * fdl_sgemm_workspace_size exceeds it returns FDL_ERROR_INVALID_VALUE.
+ * Every call on one GPU shares that GPU's scratch: calls whose work overlaps
+ * on one GPU (on different streams, or from different threads without
+ * ordering between their streams) race and may return wrong results.
+ * Results equal fdl_sgemm_ex_ws's bit for bit.
+ */
+int fdl_sgemm_ex_noalloc(int transA, int transB,
+                         int64_t M, int64_t N, int64_t K,
+                         const float* A, int64_t lda, int64_t strideA,
+                         const float* B, int64_t ldb, int64_t strideB,
+                         float* C, int64_t ldc, int64_t strideC,
+                         int64_t batch,
+                         const float* bias, const float* aux, int epilogue,
+                         void* stream);
+
+/*
  * C[m,n] = A[m,k] . B[k,n], row-major, contiguous, null stream.
  * Same contract as dl::kernels::gemm (include/dl/kernels/gemm.hpp:16-17,
  * src/kernels/cuda/gemm.cu:197-213) with the algorithm choice internal.
