@@ -379,9 +379,49 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
                       nullptr, FDL_EPILOGUE_BIAS_RELU, stream);
     if (st) return st;
 
-    // Four launches when the head fits one block per kHeadRows rows (W2 in
-    // LDS) and its per-block records fit in dW1, which holds them until the
-    // last launch overwrites it with the weight gradient.  Every parameter is
+    // Three launches when dX's product can join the head (or dX is not
+    // asked for): launch 2 makes logits, G2, G1 and dX = G1 W1^T; launch 3
+    // makes dW1 = X^T G1 with the W1 step in its epilogue, db1 with the b1
+    // step, dW2 = H^T G2 with the W2 step, and the loss, db2 and the b2 step
+    // from the stored logits and G2.  Every parameter is updated in a later
+    // launch than its last read: W1 is read by launches 1 and 2, b1 by
+    // launch 1, W2 and b2 by launch 2; all four are updated in launch 3.
+    const bool three = Cc <= fdl::kXentFusedMaxClasses &&
+                       (dX ? fdl::head_dx_supported(B, I, Hd, Cc, W1)
+                           : fdl::head_supported(Hd, Cc) &&
+                                 fdl::head_blocks(B) * (Cc + 1) <= I * Hd);
+    if (three) {
+        if (dX) {
+            st = check_hip(fdl::launch_mlp_head_dx(H, W2, b2, labels, W1, logits, G2, G1, dX, B,
+                                                   I, Hd, Cc, hs),
+                           "mlp2_train_step head failed");
+        } else {
+            // the head's records land in dW1, which launch 3 overwrites unread
+            st = check_hip(fdl::launch_mlp_head(H, W2, b2, labels, logits, G2, G1, dW1, B, Hd,
+                                                Cc, hs),
+                           "mlp2_train_step head failed");
+        }
+        if (st) return st;
+        fdl::GroupJob fin;
+        fin.kind = fdl::GroupJob::kHeadFinalize;
+        fin.x = logits;
+        fin.x2 = G2;
+        fin.labels = labels;
+        fin.out = db2;
+        fin.out2 = loss;
+        fin.param = b2;
+        fin.lr = lr;
+        fin.rows = B;
+        fin.cols = Cc;
+        const fdl::GroupJob jobs[4] = {
+            gemm_job(true, false, I, Hd, B, X, I, G1, Hd, dW1, fdl::EPI_SGD, nullptr, W1), db1_job,
+            gemm_job(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2, fdl::EPI_SGD, nullptr, W2), fin};
+        return check_hip(fdl::launch_group(jobs, 4, hs), "mlp2_train_step backward failed");
+    }
+
+    // Otherwise four launches when the head fits one block per kHeadRows rows
+    // (W2 in LDS) and its per-block records fit in dW1, which holds them until
+    // the last launch overwrites it with the weight gradient.  Every parameter is
     // updated in a later launch than its last read: b2 and W2 are read by the
     // head (launch 2), b2 is updated in launch 3 and W2 in launch 4; b1 is
     // read by launch 1 and updated in launch 3; W1 is read by launch 1 and by

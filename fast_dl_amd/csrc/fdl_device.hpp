@@ -99,6 +99,48 @@ __device__ __forceinline__ void xent_finalize_body(const float* __restrict__ par
     }
 }
 
+// The MLP head's reductions from its stored outputs (one block of 256
+// threads, classes <= kColsumCols): db = column sums of G (colsum_body, with
+// the bias step bparam -= lr * db), and the loss, each row's share
+// (logf(sum_c expf(z_c - max)) + max - z_label) / rows computed from its
+// stored logits z as the head computes it (classes in order; rows with a
+// label outside [0, classes) add nothing), shares summed in row order per
+// thread, the 256 thread sums in thread order.
+__device__ __forceinline__ void head_finalize_body(const float* __restrict__ logits,
+                                                   const float* __restrict__ g,
+                                                   const int64_t* __restrict__ labels,
+                                                   int64_t rows, int64_t classes,
+                                                   float* __restrict__ loss,
+                                                   float* __restrict__ db,
+                                                   float* __restrict__ bparam, float lr) {
+    colsum_body(g, db, bparam, lr, rows, classes, 0);
+    if (!loss) return;
+    __shared__ float lpart[kColsumThreads];
+    const int t = threadIdx.x;
+    float s = 0.0f;
+    {
+#pragma clang fp contract(off)
+        const float inv_b = 1.0f / (float)rows;
+        for (int64_t r = t; r < rows; r += kColsumThreads) {
+            const float* z = logits + r * classes;
+            const int64_t label = labels[r];
+            float mx = z[0];
+            for (int64_t c = 1; c < classes; ++c) mx = fmaxf(mx, z[c]);
+            float e = 0.0f;
+            for (int64_t c = 0; c < classes; ++c) e += expf(z[c] - mx);
+            if (label >= 0 && label < classes) s += (logf(e) + mx - z[label]) * inv_b;
+        }
+    }
+    lpart[t] = s;
+    __syncthreads();
+    if (t == 0) {
+#pragma clang fp contract(off)
+        float l = 0.0f;
+        for (int i = 0; i < kColsumThreads; ++i) l += lpart[i];
+        loss[0] = l;
+    }
+}
+
 // p[i] -= lr * g[i] over a grid-stride range; the product is rounded before
 // the subtraction (no FMA contraction), as in the reference's host update.
 __device__ __forceinline__ void sgd_body(float* __restrict__ p, const float* __restrict__ g,

@@ -68,28 +68,34 @@ bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool tra
 
 // One job of a grouped launch (launch_group): a split-K GEMM (32x32 output
 // tiles, four waves per block, any epilogue), a column sum with the bias SGD
-// step, an SGD update p -= lr * g, or the final reduction of the MLP head's
-// partial records (xent_finalize_body).
+// step, an SGD update p -= lr * g, the final reduction of the MLP head's
+// partial records (xent_finalize_body), or the head's loss, db2 and b2 step
+// from its stored logits and G2 (head_finalize_body).
 struct GroupJob {
-    enum Kind { kGemm, kColsumSgd, kSgd, kXentFinalize };
+    enum Kind { kGemm, kColsumSgd, kSgd, kXentFinalize, kHeadFinalize };
     Kind kind = kGemm;
     GemmParams p{};              // kGemm
     bool ta = false, tb = false;
     const float* x = nullptr;    // kColsumSgd: rows x cols input; kSgd: gradient;
-                                 // kXentFinalize: the partial records
-    float* out = nullptr;        // kColsumSgd, kXentFinalize: column sums (db)
-    float* out2 = nullptr;       // kXentFinalize: loss
-    float* param = nullptr;      // kColsumSgd, kSgd, kXentFinalize: the parameter updated
+                                 // kXentFinalize: the partial records;
+                                 // kHeadFinalize: logits
+    const float* x2 = nullptr;   // kHeadFinalize: G2
+    const int64_t* labels = nullptr;  // kHeadFinalize
+    float* out = nullptr;        // kColsumSgd, kXentFinalize, kHeadFinalize: column sums (db)
+    float* out2 = nullptr;       // kXentFinalize, kHeadFinalize: loss
+    float* param = nullptr;      // kColsumSgd, kSgd, k*Finalize: the parameter updated
     float lr = 0.0f;
     int64_t rows = 0, cols = 0;  // kSgd: rows is the element count;
-                                 // kXentFinalize: records, classes
+                                 // kXentFinalize: records, classes;
+                                 // kHeadFinalize: batch, classes (<= 32)
 };
 
 // Runs n (2 to 4) independent jobs in one launch, job 0 on the first blocks
 // of the grid.  Supported sequences are the ones the MLP step uses:
 // (NT GEMM, TN GEMM), (NT GEMM, column sum), (TN GEMM, SGD),
-// (NT GEMM, column sum, TN GEMM, finalize) and (column sum, TN GEMM,
-// finalize); others return hipErrorInvalidValue.
+// (NT GEMM, column sum, TN GEMM, finalize), (column sum, TN GEMM,
+// finalize) and (TN GEMM, column sum, TN GEMM, head finalize); others return
+// hipErrorInvalidValue.
 hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream);
 inline hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream) {
     const GroupJob jobs[2] = {j0, j1};
@@ -166,6 +172,24 @@ hipError_t launch_mlp_head(const float* H, const float* W2, const float* b2,
                            const int64_t* labels, float* logits, float* G2, float* G1,
                            float* part, int64_t batch, int64_t hidden, int64_t classes,
                            hipStream_t stream);
+// The head fused with dX = G1 W1^T (mlp_head_dx_kernel): kHdxRows rows and
+// kHdxCols columns of dX per block, each block recomputing the head for its
+// rows; the blocks of the first column chunk store logits, G2 and G1.  No
+// loss and no records: the loss, db2 and the b2 step come from the stored
+// logits and G2 (head_finalize_body).  Needs hidden <= 256 with hidden % 4
+// == 0, classes <= 32 and W1 16-byte aligned.
+constexpr int kHdxRows = 16;
+constexpr int kHdxCols = 64;
+inline bool head_dx_supported(int64_t batch, int64_t in_features, int64_t hidden,
+                              int64_t classes, const float* W1) {
+    return batch >= 1 && (batch + kHdxRows - 1) / kHdxRows <= 65535 && in_features >= 1 &&
+           in_features <= INT32_MAX && hidden >= 4 && hidden <= 256 && hidden % 4 == 0 &&
+           classes >= 1 && classes <= 32 && (reinterpret_cast<uintptr_t>(W1) & 15u) == 0;
+}
+hipError_t launch_mlp_head_dx(const float* H, const float* W2, const float* b2,
+                              const int64_t* labels, const float* W1, float* logits, float* G2,
+                              float* G1, float* dX, int64_t batch, int64_t in_features,
+                              int64_t hidden, int64_t classes, hipStream_t stream);
 hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,
                       hipStream_t stream);
 // Up to four (param, grad, n) updates in one launch.

@@ -453,6 +453,182 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
     }
 }
 
+// The head fused with dX = G1 W1^T (the NT product of the legacy backward,
+// legacy/src/ops/Layers.cpp:36-40), so that the W1 step can share the next
+// launch with dW1: dX's last read of W1 is in this launch.  A block takes
+// kHdxRows rows and kHdxCols columns of dX.  It first recomputes the head for
+// its rows exactly as mlp_head_kernel does, one half-wave per row (logits,
+// loss shares, G2 and G1 = (G2 W2^T) * [H > 0]); the blocks of column chunk
+// 0 store logits, G2 and G1.  Then the 16 x 64 tile of dX on
+// v_mfma_f32_16x16x4_f32:
+//   operand a: lane l supplies A[i = l % 16][k] (G1 from LDS)
+//   operand b: lane l supplies B[k][j = l % 16] = W1[col j][k]
+//   result   : lane l, register r holds D[4 * (l / 16) + r][l % 16]
+// with the k permutation of the split-K kernels (at step s of a group of 16,
+// lane quarter q supplies k0 + 4q + s, so a lane's four values are one
+// 16-byte load).  Wave w takes column tile w & 3 and half w >> 2 of the
+// hidden range; the upper half's sums reach the lower half's wave through
+// LDS and are added second.  W1's fragments are loaded at kernel start, so
+// their latency overlaps the head.  Needs hidden <= 256, hidden % 4 == 0 and
+// W1 16-byte aligned (the host checks).
+constexpr int kHdxThreads = kHdxRows * 32;
+constexpr int kWave = 64;
+
+template <int CM>
+__global__ void __launch_bounds__(kHdxThreads)
+mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
+                   const float* __restrict__ b2, const int64_t* __restrict__ labels,
+                   const float* __restrict__ W1, float* __restrict__ logits,
+                   float* __restrict__ G2, float* __restrict__ G1, float* __restrict__ dX,
+                   int batch, int in_features, int hidden, int classes) {
+    constexpr int NH = 8;                        // hidden <= 32 * NH = 256
+    constexpr int JR = 32 * NH;                  // W2 rows staged, G1 columns kept
+    constexpr int LR = CM + 4;                   // w2s row stride (as mlp_head_kernel)
+    constexpr int GR = JR + 4;                   // g1s row stride: the 16 rows of a
+                                                 // fragment read fall on distinct banks
+    constexpr int kPerThread = JR * CM / kHdxThreads;  // W2 floats staged per thread
+    constexpr int KH = JR / 2;                   // hidden range of one wave
+    constexpr int NG = KH / 16;                  // its groups of 16
+    __shared__ __attribute__((aligned(16))) float w2s[JR * LR];
+    __shared__ __attribute__((aligned(16))) float g1s[kHdxRows * GR];
+    __shared__ __attribute__((aligned(16))) floatx4 red[4][kWave];
+    __shared__ float b2s[CM];
+    __shared__ float g2s[kHdxRows][CM];
+    const int t = threadIdx.x;
+    const int lane = t & 31;
+    const int rl = t >> 5;
+    const int chunk = blockIdx.x;
+    const int row = blockIdx.y * kHdxRows + rl;
+    const bool live = row < batch;
+    const int rowc = live ? row : batch - 1;
+    const bool store_head = chunk == 0;
+
+    // The head's loads, as mlp_head_kernel: unconditional, clamped, zeroed
+    // by selects afterwards.
+    const int64_t label = labels[rowc];
+    const float* hrow = H + (int64_t)rowc * hidden;
+    float h[NH];
+#pragma unroll
+    for (int k = 0; k < NH; ++k) h[k] = hrow[min(lane + 32 * k, hidden - 1)];
+    const float b2v = b2[min(t, classes - 1)];
+    float v[kPerThread];
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+        const int e = u * kHdxThreads + t;
+        const int j = e / CM, c = e % CM;
+        v[u] = W2[min(j, hidden - 1) * classes + min(c, classes - 1)];
+    }
+    // dX operand b: this lane's W1 fragments, issued after the head's loads
+    // (loads complete in order, so the W2 staging below waits only for the
+    // head's) and before anything else waits.
+    const int l64 = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int ct = wave & 3;
+    const int kh = wave >> 2;
+    const int q = l64 >> 4;
+    const int col = chunk * kHdxCols + ct * 16 + (l64 & 15);
+    const float* w1row = W1 + (int64_t)min(col, in_features - 1) * hidden;
+    floatx4 wb[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int k0 = kh * KH + 16 * g + 4 * q;
+        wb[g] = *reinterpret_cast<const floatx4*>(w1row + min(k0, hidden - 4));
+    }
+    // (fragments past `hidden` are zeroed where they are used, after the head:
+    // a select here would make the compiler wait for the loads first)
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+        const int e = u * kHdxThreads + t;
+        const int j = e / CM, c = e % CM;
+        w2s[j * LR + c] = (j < hidden && c < classes) ? v[u] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < NH; ++k) h[k] = lane + 32 * k < hidden ? h[k] : 0.0f;
+    if (t < CM) b2s[t] = t < classes ? b2v : 0.0f;
+    __syncthreads();
+
+    float z[CM];
+#pragma unroll
+    for (int c = 0; c < CM; ++c) z[c] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+        const float* w = w2s + (lane + 32 * k) * LR;
+#pragma unroll
+        for (int c = 0; c < CM; ++c) z[c] = fmaf(h[k], w[c], z[c]);
+    }
+    const int c = CM == 32 ? lane : lane >> 1;
+    const bool owner = CM == 32 || (lane & 1) == 0;
+    const bool cls = c < classes;
+    float zc = transpose_sum<CM>(z, lane);
+    float gc;
+    {
+#pragma clang fp contract(off)
+        const float inv_b = 1.0f / (float)batch;
+        zc = zc + b2s[c];
+        const float mx = half_wave_max(cls ? zc : -INFINITY);
+        const float ez = cls ? expf(zc - mx) : 0.0f;
+        const float s = half_wave_sum(owner ? ez : 0.0f);
+        const bool valid = label >= 0 && label < classes;
+        const float inv_s = 1.0f / s;
+        float pc = cls ? ez * inv_s : 0.0f;
+        if (valid && c == label) pc -= 1.0f;
+        gc = pc * inv_b;
+    }
+    if (owner && cls) {
+        if (live && store_head) {
+            logits[(int64_t)row * classes + c] = zc;
+            G2[(int64_t)row * classes + c] = gc;
+        }
+        g2s[rl][c] = live ? gc : 0.0f;
+    }
+    if (owner && !cls && c < CM) g2s[rl][c] = 0.0f;
+    __syncthreads();
+
+    // G1 row into LDS (zero past `hidden` and for rows past the batch).
+    float g[CM];
+#pragma unroll
+    for (int qq = 0; qq < CM; ++qq) g[qq] = g2s[rl][qq];
+    float* g1row = G1 + (int64_t)rowc * hidden;
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+        const int j = lane + 32 * k;
+        const float* w = w2s + j * LR;
+        float v = 0.0f;
+#pragma unroll
+        for (int qq = 0; qq < CM; ++qq) v = fmaf(g[qq], w[qq], v);
+        const float g1 = (live && j < hidden && h[k] > 0.0f) ? v : 0.0f;
+        g1s[rl * GR + j] = g1;
+        if (live && store_head && j < hidden) g1row[j] = g1;
+    }
+    __syncthreads();
+
+    // dX tile: 16 rows x 16 columns per wave over its half of the hidden range.
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* arow = g1s + (l64 & 15) * GR + kh * KH + 4 * q;
+#pragma unroll
+    for (int gg = 0; gg < NG; ++gg) {
+        const floatx4 a = *reinterpret_cast<const floatx4*>(arow + 16 * gg);
+        const bool in_k = kh * KH + 16 * gg + 4 * q < hidden;
+        const floatx4 b = in_k ? wb[gg] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
+        }
+    }
+    if (kh == 1) red[ct][l64] = acc;
+    __syncthreads();
+    if (kh == 0) {
+        const floatx4 up = red[ct][l64];
+        if (col < in_features) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int orow = blockIdx.y * kHdxRows + 4 * q + r;
+                if (orow < batch) dX[(int64_t)orow * in_features + col] = acc[r] + up[r];
+            }
+        }
+    }
+}
+
 // p -= lr * g with the product rounded before the subtraction (no FMA
 // contraction), as the reference's x86 host update computes it.
 __global__ void sgd_kernel(float* __restrict__ p, const float* __restrict__ g,
@@ -633,6 +809,25 @@ hipError_t launch_mlp_head(const float* H, const float* W2, const float* b2,
                                                       batch, hidden, classes, stream)
                          : launch_mlp_head_cfg<32, 16>(H, W2, b2, labels, logits, G2, G1, part,
                                                        batch, hidden, classes, stream);
+}
+
+hipError_t launch_mlp_head_dx(const float* H, const float* W2, const float* b2,
+                              const int64_t* labels, const float* W1, float* logits, float* G2,
+                              float* G1, float* dX, int64_t batch, int64_t in_features,
+                              int64_t hidden, int64_t classes, hipStream_t stream) {
+    if (!head_dx_supported(batch, in_features, hidden, classes, W1)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((in_features + kHdxCols - 1) / kHdxCols),
+                    (unsigned)((batch + kHdxRows - 1) / kHdxRows));
+    if (classes <= 16) {
+        hipLaunchKernelGGL((mlp_head_dx_kernel<16>), grid, dim3(kHdxThreads), 0, stream, H, W2,
+                           b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
+                           (int)hidden, (int)classes);
+    } else {
+        hipLaunchKernelGGL((mlp_head_dx_kernel<32>), grid, dim3(kHdxThreads), 0, stream, H, W2,
+                           b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
+                           (int)hidden, (int)classes);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,

@@ -1749,6 +1749,8 @@ struct GroupDev {
     GemmParams p;
     int tiles_m, tiles_n, kchunk, blocks;
     const float* x;
+    const float* x2;
+    const int64_t* labels;
     float* out;
     float* out2;
     float* param;
@@ -1788,6 +1790,12 @@ struct JobSgd {
 struct JobXentFinalize {
     static __device__ __forceinline__ void run(const GroupDev& a, int) {
         xent_finalize_body(a.x, (int)a.rows, (int)a.cols, a.out2, a.out, a.param, a.lr);
+    }
+};
+
+struct JobHeadFinalize {
+    static __device__ __forceinline__ void run(const GroupDev& a, int) {
+        head_finalize_body(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out, a.param, a.lr);
     }
 };
 
@@ -2167,6 +2175,8 @@ GroupDev group_dev(const GroupJob& j) {
     GroupDev d{};
     d.p = j.p;
     d.x = j.x;
+    d.x2 = j.x2;
+    d.labels = j.labels;
     d.out = j.out;
     d.out2 = j.out2;
     d.param = j.param;
@@ -2190,6 +2200,7 @@ GroupDev group_dev(const GroupJob& j) {
             d.blocks = (int)std::min<int64_t>((j.rows + 4 * 256 - 1) / (4 * 256), 1024);
             break;
         case GroupJob::kXentFinalize:
+        case GroupJob::kHeadFinalize:
             d.blocks = 1;
             break;
     }
@@ -2227,6 +2238,10 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
         if (j.kind == GroupJob::kGemm && (j.p.M <= 0 || j.p.N <= 0 || j.p.K <= 0)) {
             return hipErrorInvalidValue;
         }
+        if (j.kind == GroupJob::kHeadFinalize &&
+            (j.rows <= 0 || j.cols <= 0 || j.cols > kColsumCols)) {
+            return hipErrorInvalidValue;
+        }
         a.d[i] = group_dev(j);
     }
     auto is_nt = [&](int i) {
@@ -2251,6 +2266,10 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
         if (is_nt(0) && is(1, GroupJob::kColsumSgd) && is_tn(2) &&
             is(3, GroupJob::kXentFinalize)) {
             return launch_nt_first<JobColsumSgd, TN, JobXentFinalize>(jobs[0], a, stream);
+        }
+        if (is_tn(0) && is(1, GroupJob::kColsumSgd) && is_tn(2) &&
+            is(3, GroupJob::kHeadFinalize)) {
+            return launch_group_of<TN, JobColsumSgd, TN, JobHeadFinalize>(a, stream);
         }
     }
     return hipErrorInvalidValue;
