@@ -387,7 +387,7 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
     // launch than its last read: W1 is read by launches 1 and 2, b1 by
     // launch 1, W2 and b2 by launch 2; all four are updated in launch 3.
     const bool three = Cc <= fdl::kXentFusedMaxClasses &&
-                       (dX ? fdl::head_dx_supported(B, I, Hd, Cc, W1)
+                       (dX ? fdl::head_dx_supported(B, I, Hd, Cc, H, W1)
                            : fdl::head_supported(Hd, Cc) &&
                                  fdl::head_blocks(B) * (Cc + 1) <= I * Hd);
     if (three) {

@@ -177,14 +177,15 @@ hipError_t launch_mlp_head(const float* H, const float* W2, const float* b2,
 // rows; the blocks of the first column chunk store logits, G2 and G1.  No
 // loss and no records: the loss, db2 and the b2 step come from the stored
 // logits and G2 (head_finalize_body).  Needs hidden <= 256 with hidden % 4
-// == 0, classes <= 32 and W1 16-byte aligned.
+// == 0, classes <= 32, and H and W1 16-byte aligned.
 constexpr int kHdxRows = 16;
 constexpr int kHdxCols = 64;
 inline bool head_dx_supported(int64_t batch, int64_t in_features, int64_t hidden,
-                              int64_t classes, const float* W1) {
+                              int64_t classes, const float* H, const float* W1) {
     return batch >= 1 && (batch + kHdxRows - 1) / kHdxRows <= 65535 && in_features >= 1 &&
            in_features <= INT32_MAX && hidden >= 4 && hidden <= 256 && hidden % 4 == 0 &&
-           classes >= 1 && classes <= 32 && (reinterpret_cast<uintptr_t>(W1) & 15u) == 0;
+           classes >= 1 && classes <= 32 && (reinterpret_cast<uintptr_t>(H) & 15u) == 0 &&
+           (reinterpret_cast<uintptr_t>(W1) & 15u) == 0;
 }
 hipError_t launch_mlp_head_dx(const float* H, const float* W2, const float* b2,
                               const int64_t* labels, const float* W1, float* logits, float* G2,

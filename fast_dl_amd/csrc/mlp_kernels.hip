@@ -453,64 +453,99 @@ mlp_head_kernel(const float* __restrict__ H, const float* __restrict__ W2,
     }
 }
 
+// Reductions over the 16 lanes of a DPP row (steps 1 to 4 of the half-wave
+// exchanges), leaving the result on every lane of the row.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, half_wave_partner<1>(x));
+    x = fmaxf(x, half_wave_partner<2>(x));
+    x = fmaxf(x, half_wave_partner<3>(x));
+    return fmaxf(x, half_wave_partner<4>(x));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+    x += half_wave_partner<1>(x);
+    x += half_wave_partner<2>(x);
+    x += half_wave_partner<3>(x);
+    return x + half_wave_partner<4>(x);
+}
+
 // The head fused with dX = G1 W1^T (the NT product of the legacy backward,
 // legacy/src/ops/Layers.cpp:36-40), so that the W1 step can share the next
 // launch with dW1: dX's last read of W1 is in this launch.  A block takes
-// kHdxRows rows and kHdxCols columns of dX.  It first recomputes the head for
-// its rows exactly as mlp_head_kernel does, one half-wave per row (logits,
-// loss shares, G2 and G1 = (G2 W2^T) * [H > 0]); the blocks of column chunk
-// 0 store logits, G2 and G1.  Then the 16 x 64 tile of dX on
+// kHdxRows = 16 rows of the batch and kHdxCols = 64 columns of dX; every
+// block recomputes the head for its rows and the blocks of column chunk 0
+// store logits, G2 and G1.  All three products run on
 // v_mfma_f32_16x16x4_f32:
-//   operand a: lane l supplies A[i = l % 16][k] (G1 from LDS)
-//   operand b: lane l supplies B[k][j = l % 16] = W1[col j][k]
+//   operand a: lane l supplies A[i = l % 16][k]
+//   operand b: lane l supplies B[k][j = l % 16]
 //   result   : lane l, register r holds D[4 * (l / 16) + r][l % 16]
 // with the k permutation of the split-K kernels (at step s of a group of 16,
 // lane quarter q supplies k0 + 4q + s, so a lane's four values are one
-// 16-byte load).  Wave w takes column tile w & 3 and half w >> 2 of the
-// hidden range; the upper half's sums reach the lower half's wave through
-// LDS and are added second.  W1's fragments are loaded at kernel start, so
-// their latency overlaps the head.  Needs hidden <= 256, hidden % 4 == 0 and
-// W1 16-byte aligned (the host checks).
+// 16-byte load).
+//   z = H W2 (16 rows x CT tiles of 16 classes): wave w adds hidden
+//     [32w, 32w + 32) straight from H's rows; the eight waves' tiles meet in
+//     LDS and wave 0 adds them in wave order, adds b2 after the sum (as
+//     linear_cpu, tests/tensor/linear_tensor_test.cpp:17-25), and takes the
+//     softmax of each row over the 16 lanes of a DPP row: G2 as
+//     softmax_xent_kernel (legacy SoftmaxCrossEntropyLoss,
+//     legacy/src/ops/SoftmaxCrossEntropyLoss.cpp:39-51).  The loss is left to
+//     head_finalize_body, which reads the stored logits.
+//   G1 = (G2 W2^T) * [H > 0] (legacy/src/ops/Layers.cpp:36 through the ReLU
+//     mask): wave w makes hidden tiles 2w and 2w + 1, K = the classes.
+//   dX = G1 W1^T: wave w makes column tile w % NCT over part w / NCT of the
+//     hidden range; the other parts' sums reach part 0's wave through LDS
+//     and are added in part order.
+// W2 is staged in LDS as rows of CM floats (stride CM + 4), zero past
+// `hidden` rows and `classes` columns.  Every global load is issued before
+// the first wait (the W1 fragments last: loads complete in order, so the
+// staging waits only for the loads before them), at addresses clamped into
+// the arrays, and values outside the problem are zeroed where they are used.
+// Needs hidden <= 256, hidden % 4 == 0, classes <= 16 * CT, and H and W1
+// 16-byte aligned (the host checks).
 constexpr int kHdxThreads = kHdxRows * 32;
 constexpr int kWave = 64;
 
-template <int CM>
+template <int CT>
 __global__ void __launch_bounds__(kHdxThreads)
 mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
                    const float* __restrict__ b2, const int64_t* __restrict__ labels,
                    const float* __restrict__ W1, float* __restrict__ logits,
                    float* __restrict__ G2, float* __restrict__ G1, float* __restrict__ dX,
                    int batch, int in_features, int hidden, int classes) {
-    constexpr int NH = 8;                        // hidden <= 32 * NH = 256
-    constexpr int JR = 32 * NH;                  // W2 rows staged, G1 columns kept
-    constexpr int LR = CM + 4;                   // w2s row stride (as mlp_head_kernel)
-    constexpr int GR = JR + 4;                   // g1s row stride: the 16 rows of a
-                                                 // fragment read fall on distinct banks
+    constexpr int CM = 16 * CT;                  // classes padded to whole tiles
+    constexpr int JR = 256;                      // hidden <= JR
+    constexpr int LR = CM + 4;                   // w2s row stride: the 16 rows of a
+                                                 // 16-byte fragment read on distinct banks
+    constexpr int GR = JR + 4;                   // g1s row stride, same reason
+    constexpr int NW = kHdxThreads / kWave;      // 8 waves
+    constexpr int KZ = JR / NW;                  // hidden range of a wave for z
+    constexpr int NCT = kHdxCols / 16;           // dX column tiles of a block
+    constexpr int NKS = NW / NCT;                // hidden range split in NKS parts
+    constexpr int KH = JR / NKS;                 // hidden range of a wave for dX
+    constexpr int NG = KH / 16;
     constexpr int kPerThread = JR * CM / kHdxThreads;  // W2 floats staged per thread
-    constexpr int KH = JR / 2;                   // hidden range of one wave
-    constexpr int NG = KH / 16;                  // its groups of 16
+    static_assert(KZ == 32 && NW == 8, "z takes two groups of 16 per wave");
     __shared__ __attribute__((aligned(16))) float w2s[JR * LR];
     __shared__ __attribute__((aligned(16))) float g1s[kHdxRows * GR];
-    __shared__ __attribute__((aligned(16))) floatx4 red[4][kWave];
+    __shared__ __attribute__((aligned(16))) float g2s[kHdxRows * LR];
+    __shared__ __attribute__((aligned(16))) floatx4 zred[NW][CT][kWave];
+    __shared__ __attribute__((aligned(16))) floatx4 red[NKS - 1][NCT][kWave];
+    __shared__ int64_t lbls[kHdxRows];
     __shared__ float b2s[CM];
-    __shared__ float g2s[kHdxRows][CM];
     const int t = threadIdx.x;
-    const int lane = t & 31;
-    const int rl = t >> 5;
+    const int l64 = t & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int q = l64 >> 4;
+    const int i16 = l64 & 15;
     const int chunk = blockIdx.x;
-    const int row = blockIdx.y * kHdxRows + rl;
-    const bool live = row < batch;
-    const int rowc = live ? row : batch - 1;
+    const int r0 = blockIdx.y * kHdxRows;
     const bool store_head = chunk == 0;
 
-    // The head's loads, as mlp_head_kernel: unconditional, clamped, zeroed
-    // by selects afterwards.
-    const int64_t label = labels[rowc];
-    const float* hrow = H + (int64_t)rowc * hidden;
-    float h[NH];
-#pragma unroll
-    for (int k = 0; k < NH; ++k) h[k] = hrow[min(lane + 32 * k, hidden - 1)];
-    const float b2v = b2[min(t, classes - 1)];
+    // ---- loads ----
+    // softmax inputs, staged in LDS with W2 (a load used only inside the
+    // softmax branch would be issued there, a round trip late)
+    const int64_t lab_t = labels[min(r0 + (t & (kHdxRows - 1)), batch - 1)];
+    const float b2_t = b2[min(t & (CM - 1), classes - 1)];
     float v[kPerThread];
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
@@ -518,112 +553,158 @@ mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
         const int j = e / CM, c = e % CM;
         v[u] = W2[min(j, hidden - 1) * classes + min(c, classes - 1)];
     }
-    // dX operand b: this lane's W1 fragments, issued after the head's loads
-    // (loads complete in order, so the W2 staging below waits only for the
-    // head's) and before anything else waits.
-    const int l64 = t & (kWave - 1);
-    const int wave = t / kWave;
-    const int ct = wave & 3;
-    const int kh = wave >> 2;
-    const int q = l64 >> 4;
-    const int col = chunk * kHdxCols + ct * 16 + (l64 & 15);
+    // z operand a: H[r0 + i16][32w + 16g + 4q .. + 3]
+    const float* harow = H + (int64_t)min(r0 + i16, batch - 1) * hidden;
+    floatx4 ha[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        ha[g] = *reinterpret_cast<const floatx4*>(harow + min(w * KZ + 16 * g + 4 * q, hidden - 4));
+    }
+    // G1's mask: H[r0 + 4q + r][16 (2w + tt) + i16]
+    float hm[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            hm[tt][r] = H[(int64_t)min(r0 + 4 * q + r, batch - 1) * hidden +
+                          min(16 * (2 * w + tt) + i16, hidden - 1)];
+    // dX operand b: W1[col][k0 .. k0 + 3]
+    const int ct4 = w % NCT;
+    const int kh = w / NCT;
+    const int col = chunk * kHdxCols + ct4 * 16 + i16;
     const float* w1row = W1 + (int64_t)min(col, in_features - 1) * hidden;
     floatx4 wb[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        const int k0 = kh * KH + 16 * g + 4 * q;
-        wb[g] = *reinterpret_cast<const floatx4*>(w1row + min(k0, hidden - 4));
+        wb[g] = *reinterpret_cast<const floatx4*>(w1row + min(kh * KH + 16 * g + 4 * q, hidden - 4));
     }
-    // (fragments past `hidden` are zeroed where they are used, after the head:
-    // a select here would make the compiler wait for the loads first)
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
         const int e = u * kHdxThreads + t;
         const int j = e / CM, c = e % CM;
         w2s[j * LR + c] = (j < hidden && c < classes) ? v[u] : 0.0f;
     }
-#pragma unroll
-    for (int k = 0; k < NH; ++k) h[k] = lane + 32 * k < hidden ? h[k] : 0.0f;
-    if (t < CM) b2s[t] = t < classes ? b2v : 0.0f;
+    // every thread stores (threads with equal indices store equal values): a
+    // store under a branch would pull its load into the branch
+    lbls[t & (kHdxRows - 1)] = lab_t;
+    b2s[t & (CM - 1)] = (t & (CM - 1)) < classes ? b2_t : 0.0f;
     __syncthreads();
 
-    float z[CM];
+    // ---- z = H W2: this wave's 32 hidden values ----
+    const floatx4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool row_in = r0 + i16 < batch;
 #pragma unroll
-    for (int c = 0; c < CM; ++c) z[c] = 0.0f;
+    for (int ct = 0; ct < CT; ++ct) {
+        floatx4 zacc = zero4;
 #pragma unroll
-    for (int k = 0; k < NH; ++k) {
-        const float* w = w2s + (lane + 32 * k) * LR;
+        for (int g = 0; g < 2; ++g) {
+            const int k0 = w * KZ + 16 * g;
+            const floatx4 a = (row_in && k0 + 4 * q < hidden) ? ha[g] : zero4;
 #pragma unroll
-        for (int c = 0; c < CM; ++c) z[c] = fmaf(h[k], w[c], z[c]);
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const float b = w2s[(k0 + 4 * q + s2) * LR + 16 * ct + i16];
+                zacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], b, zacc, 0, 0, 0);
+            }
+        }
+        zred[w][ct][l64] = zacc;
     }
-    const int c = CM == 32 ? lane : lane >> 1;
-    const bool owner = CM == 32 || (lane & 1) == 0;
-    const bool cls = c < classes;
-    float zc = transpose_sum<CM>(z, lane);
-    float gc;
-    {
+    __syncthreads();
+
+    // ---- softmax and G2: wave r (< 4) takes register r of the tiles, so a
+    // lane holds row 4q + r, class 16 ct + i16, and a DPP row of 16 lanes one
+    // row of the batch ----
+    if (w < 4) {
 #pragma clang fp contract(off)
-        const float inv_b = 1.0f / (float)batch;
-        zc = zc + b2s[c];
-        const float mx = half_wave_max(cls ? zc : -INFINITY);
-        const float ez = cls ? expf(zc - mx) : 0.0f;
-        const float s = half_wave_sum(owner ? ez : 0.0f);
+        const int r = w;
+        float zc[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            float zz = zred[0][ct][l64][r];
+#pragma unroll
+            for (int ww = 1; ww < NW; ++ww) zz += zred[ww][ct][l64][r];
+            zc[ct] = zz + b2s[16 * ct + i16];
+        }
+        const int row = r0 + 4 * q + r;
+        const bool live = row < batch;
+        const int64_t label = lbls[4 * q + r];
         const bool valid = label >= 0 && label < classes;
-        const float inv_s = 1.0f / s;
-        float pc = cls ? ez * inv_s : 0.0f;
-        if (valid && c == label) pc -= 1.0f;
-        gc = pc * inv_b;
-    }
-    if (owner && cls) {
-        if (live && store_head) {
-            logits[(int64_t)row * classes + c] = zc;
-            G2[(int64_t)row * classes + c] = gc;
+        const float inv_b = 1.0f / (float)batch;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            if (16 * ct + i16 < classes) mx = fmaxf(mx, zc[ct]);
         }
-        g2s[rl][c] = live ? gc : 0.0f;
-    }
-    if (owner && !cls && c < CM) g2s[rl][c] = 0.0f;
-    __syncthreads();
-
-    // G1 row into LDS (zero past `hidden` and for rows past the batch).
-    float g[CM];
+        mx = row16_max(mx);
+        float ez[CT];
+        float es = 0.0f;
 #pragma unroll
-    for (int qq = 0; qq < CM; ++qq) g[qq] = g2s[rl][qq];
-    float* g1row = G1 + (int64_t)rowc * hidden;
+        for (int ct = 0; ct < CT; ++ct) {
+            ez[ct] = 16 * ct + i16 < classes ? expf(zc[ct] - mx) : 0.0f;
+            es += ez[ct];
+        }
+        const float inv_s = 1.0f / row16_sum(es);
 #pragma unroll
-    for (int k = 0; k < NH; ++k) {
-        const int j = lane + 32 * k;
-        const float* w = w2s + j * LR;
-        float v = 0.0f;
-#pragma unroll
-        for (int qq = 0; qq < CM; ++qq) v = fmaf(g[qq], w[qq], v);
-        const float g1 = (live && j < hidden && h[k] > 0.0f) ? v : 0.0f;
-        g1s[rl * GR + j] = g1;
-        if (live && store_head && j < hidden) g1row[j] = g1;
+        for (int ct = 0; ct < CT; ++ct) {
+            const int c = 16 * ct + i16;
+            float pc = ez[ct] * inv_s;
+            if (valid && c == label) pc -= 1.0f;
+            const float gc = pc * inv_b;
+            if (live && store_head && c < classes) {
+                logits[(int64_t)row * classes + c] = zc[ct];
+                G2[(int64_t)row * classes + c] = gc;
+            }
+            g2s[(4 * q + r) * LR + c] = (live && c < classes) ? gc : 0.0f;
+        }
     }
     __syncthreads();
 
-    // dX tile: 16 rows x 16 columns per wave over its half of the hidden range.
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* arow = g1s + (l64 & 15) * GR + kh * KH + 4 * q;
+    // ---- G1 = (G2 W2^T) * [H > 0]: hidden tiles 2w and 2w + 1 ----
 #pragma unroll
-    for (int gg = 0; gg < NG; ++gg) {
-        const floatx4 a = *reinterpret_cast<const floatx4*>(arow + 16 * gg);
-        const bool in_k = kh * KH + 16 * gg + 4 * q < hidden;
-        const floatx4 b = in_k ? wb[gg] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < 2; ++tt) {
+        const int j = 16 * (2 * w + tt) + i16;
+        floatx4 gacc = zero4;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
+        for (int g = 0; g < CT; ++g) {
+            const floatx4 a = *reinterpret_cast<const floatx4*>(g2s + i16 * LR + 16 * g + 4 * q);
+            const floatx4 b = *reinterpret_cast<const floatx4*>(w2s + j * LR + 16 * g + 4 * q);
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                gacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], b[s2], gacc, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = r0 + 4 * q + r;
+            const bool keep = row < batch && j < hidden;
+            const float g1 = (keep && hm[tt][r] > 0.0f) ? gacc[r] : 0.0f;
+            g1s[(4 * q + r) * GR + j] = g1;
+            if (keep && store_head) G1[(int64_t)row * hidden + j] = g1;
         }
     }
-    if (kh == 1) red[ct][l64] = acc;
+    __syncthreads();
+
+    // ---- dX tile: 16 rows x 16 columns per wave over its part of the hidden range ----
+    floatx4 acc = zero4;
+    const float* arow = g1s + i16 * GR + kh * KH + 4 * q;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const floatx4 a = *reinterpret_cast<const floatx4*>(arow + 16 * g);
+        const floatx4 b = kh * KH + 16 * g + 4 * q < hidden ? wb[g] : zero4;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], b[s2], acc, 0, 0, 0);
+        }
+    }
+    if (kh > 0) red[kh - 1][ct4][l64] = acc;
     __syncthreads();
     if (kh == 0) {
-        const floatx4 up = red[ct][l64];
+#pragma unroll
+        for (int p = 0; p < NKS - 1; ++p) acc += red[p][ct4][l64];
         if (col < in_features) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int orow = blockIdx.y * kHdxRows + 4 * q + r;
-                if (orow < batch) dX[(int64_t)orow * in_features + col] = acc[r] + up[r];
+                const int orow = r0 + 4 * q + r;
+                if (orow < batch) dX[(int64_t)orow * in_features + col] = acc[r];
             }
         }
     }
@@ -815,15 +896,15 @@ hipError_t launch_mlp_head_dx(const float* H, const float* W2, const float* b2,
                               const int64_t* labels, const float* W1, float* logits, float* G2,
                               float* G1, float* dX, int64_t batch, int64_t in_features,
                               int64_t hidden, int64_t classes, hipStream_t stream) {
-    if (!head_dx_supported(batch, in_features, hidden, classes, W1)) return hipErrorInvalidValue;
+    if (!head_dx_supported(batch, in_features, hidden, classes, H, W1)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((in_features + kHdxCols - 1) / kHdxCols),
                     (unsigned)((batch + kHdxRows - 1) / kHdxRows));
     if (classes <= 16) {
-        hipLaunchKernelGGL((mlp_head_dx_kernel<16>), grid, dim3(kHdxThreads), 0, stream, H, W2,
+        hipLaunchKernelGGL((mlp_head_dx_kernel<1>), grid, dim3(kHdxThreads), 0, stream, H, W2,
                            b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
                            (int)hidden, (int)classes);
     } else {
-        hipLaunchKernelGGL((mlp_head_dx_kernel<32>), grid, dim3(kHdxThreads), 0, stream, H, W2,
+        hipLaunchKernelGGL((mlp_head_dx_kernel<2>), grid, dim3(kHdxThreads), 0, stream, H, W2,
                            b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
                            (int)hidden, (int)classes);
     }
