@@ -343,8 +343,13 @@ def mlp_rate(capi, torch, steps=200, warmup=20):
             W2.data_ptr(), b2.data_ptr(), 0.1, p["H"], p["logits"], p["G2"], p["G1"], p["dW1"],
             p["db1"], p["dW2"], p["db2"], p["dX"], p["loss"], stream)
 
+    # The C function itself, its status checked, without the wrapper's
+    # per-call library lookup (the Python loop is the host side of the step).
+    fn = capi.load_library().fdl_mlp2_train_step
+
     def step():
-        capi.mlp2_train_step(*args)
+        if fn(*args) != 0:
+            raise capi.FdlError("fdl_mlp2_train_step", -1, capi.last_error())
 
     warm_clock(step, torch.cuda.current_stream())
     ms = time_launches(step, steps, warmup, torch.cuda.current_stream())

@@ -3,8 +3,9 @@
 Shapes are drawn across the head kernel's dispatch boundaries (classes up to
 40 against the 16- and 32-class paddings, hidden up to 1100 against the 512
 and 1024 limits, batches that are not multiples of its 8 rows, dW1 too small
-for its records) so both the four-launch and the six-launch step are reached,
-with and without dX, and some labels outside [0, classes) (left out of the
+for its records, hidden values that do and do not fit the fused head and dX
+kernel) so the three-, four- and six-launch steps are all reached, with and
+without dX, and some labels outside [0, classes) (left out of the
 loss, as the reference's cross_entropy does).  Bar: every intermediate and
 updated parameter within 1e-4 of the fp32 oracle step, normwise (the path's
 "max relative error <= 1e-4" criterion), with the products and column sums
