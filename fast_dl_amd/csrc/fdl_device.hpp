@@ -104,8 +104,12 @@ __device__ __forceinline__ void xent_finalize_body(const float* __restrict__ par
 // the bias step bparam -= lr * db), and the loss, each row's share
 // (logf(sum_c expf(z_c - max)) + max - z_label) / rows computed from its
 // stored logits z as the head computes it (classes in order; rows with a
-// label outside [0, classes) add nothing), shares summed in row order per
-// thread, the 256 thread sums in thread order.
+// label outside [0, classes) add nothing).  A thread takes rows t, t + 256,
+// ...; a row's logits and label are loaded before the column sums (all
+// kColsumCols loads at clamped addresses, so none waits on another), the
+// shares are summed in row order per thread, then over each wave by a fixed
+// exchange tree and over the waves in order.
+template <int CM>
 __device__ __forceinline__ void head_finalize_body(const float* __restrict__ logits,
                                                    const float* __restrict__ g,
                                                    const int64_t* __restrict__ labels,
@@ -113,30 +117,55 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
                                                    float* __restrict__ loss,
                                                    float* __restrict__ db,
                                                    float* __restrict__ bparam, float lr) {
+    static_assert(CM <= kColsumCols, "one block of column sums");
+    const int t = threadIdx.x;
+    const int64_t r0 = t < rows ? t : rows - 1;
+    float z[CM];
+#pragma unroll
+    for (int c = 0; c < CM; ++c) z[c] = logits[r0 * classes + (c < classes ? c : classes - 1)];
+    const int64_t label0 = labels[r0];
     colsum_body(g, db, bparam, lr, rows, classes, 0);
     if (!loss) return;
-    __shared__ float lpart[kColsumThreads];
-    const int t = threadIdx.x;
+    __shared__ float wpart[kColsumThreads / 64];
     float s = 0.0f;
     {
 #pragma clang fp contract(off)
         const float inv_b = 1.0f / (float)rows;
         for (int64_t r = t; r < rows; r += kColsumThreads) {
-            const float* z = logits + r * classes;
-            const int64_t label = labels[r];
+            int64_t label = label0;
+            if (r != t) {  // rows past the first 256: load them here
+                label = labels[r];
+#pragma unroll
+                for (int c = 0; c < CM; ++c) z[c] = logits[r * classes + (c < classes ? c : classes - 1)];
+            }
+            // `classes` is the same on every lane: the tests below are
+            // scalar branches, so padded classes cost no expf
             float mx = z[0];
-            for (int64_t c = 1; c < classes; ++c) mx = fmaxf(mx, z[c]);
+#pragma unroll
+            for (int c = 1; c < CM; ++c) {
+                if (c < classes) mx = fmaxf(mx, z[c]);
+            }
             float e = 0.0f;
-            for (int64_t c = 0; c < classes; ++c) e += expf(z[c] - mx);
-            if (label >= 0 && label < classes) s += (logf(e) + mx - z[label]) * inv_b;
+            float zl = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CM; ++c) {
+                if (c < classes) {
+                    e += expf(z[c] - mx);
+                    zl = c == label ? z[c] : zl;
+                }
+            }
+            if (label >= 0 && label < classes) s += (logf(e) + mx - zl) * inv_b;
         }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     }
-    lpart[t] = s;
+    if ((t & 63) == 0) wpart[t >> 6] = s;
     __syncthreads();
     if (t == 0) {
 #pragma clang fp contract(off)
-        float l = 0.0f;
-        for (int i = 0; i < kColsumThreads; ++i) l += lpart[i];
+        float l = wpart[0];
+#pragma unroll
+        for (int i = 1; i < kColsumThreads / 64; ++i) l += wpart[i];
         loss[0] = l;
     }
 }

@@ -1795,7 +1795,13 @@ struct JobXentFinalize {
 
 struct JobHeadFinalize {
     static __device__ __forceinline__ void run(const GroupDev& a, int) {
-        head_finalize_body(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out, a.param, a.lr);
+        if (a.cols <= 16) {
+            head_finalize_body<16>(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out, a.param,
+                                   a.lr);
+        } else {
+            head_finalize_body<kColsumCols>(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out,
+                                            a.param, a.lr);
+        }
     }
 };
 
