@@ -1557,23 +1557,54 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
         return TA ? A[(int64_t)k * p.lda + mm] : A[(int64_t)mm * p.lda + k];
     };
 
-    int k = k0 + w;
-    for (; k + NW * (UNR - 1) < k1; k += NW * UNR) {
-        floatx4 b[UNR];
-        float a[UNR][MR];
+    auto load = [&](int kk, floatx4 (&b)[UNR], float (&a)[UNR][MR]) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
-            b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(k + NW * u) * p.ldb + n0);
+            b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * p.ldb + n0);
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) a[u][m] = a_at(m, k + NW * u);
+            for (int m = 0; m < MR; ++m) a[u][m] = a_at(m, kk + NW * u);
+    };
+    auto fma_rows = [&](const floatx4 (&b)[UNR], const float (&a)[UNR][MR]) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(a[u][m], b[u][c], acc[m][c]);
+    };
+    int k = k0 + w;
+    if constexpr (MR <= 2) {
+        // Software-pipelined: the next UNR rows are in flight while this
+        // group's FMAs run (C5a M = 1: 15.9 -> 15.7 us; M = 1, N = 1024,
+        // K = 16384: 18.9 -> 17.6 us).  At M = 8 the second register set
+        // cost more than it hid (18.9 -> 23.5 us), so larger M keep one.
+        const int span = k1 - k - NW * (UNR - 1);
+        const int groups = span > 0 ? (span + NW * UNR - 1) / (NW * UNR) : 0;
+        floatx4 b0[UNR], b1[UNR];
+        float a0[UNR][MR], a1[UNR][MR];
+        if (groups > 0) load(k, b0, a0);
+        int it = 0;
+        for (; it + 2 <= groups; it += 2) {
+            load(k + NW * UNR, b1, a1);
+            fma_rows(b0, a0);
+            k += NW * UNR;
+            if (it + 2 < groups) load(k + NW * UNR, b0, a0);
+            fma_rows(b1, a1);
+            k += NW * UNR;
+        }
+        if (it < groups) {
+            fma_rows(b0, a0);
+            k += NW * UNR;
+        }
+    } else {
+        for (; k + NW * (UNR - 1) < k1; k += NW * UNR) {
+            floatx4 b[UNR];
+            float a[UNR][MR];
+            load(k, b, a);
+            fma_rows(b, a);
+        }
     }
     for (; k < k1; k += NW) {
         const floatx4 b = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + n0);
