@@ -892,11 +892,17 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                         a[slot][q][mi], b[slot][q][ni], acc[mi][ni], 0, 0, 0);
     };
+    // The fragment reads the hints below spread: FM b128 A reads and about
+    // two instructions per B fragment.  One more for the one-column-fragment
+    // tiles of the 128-row and 4-byte-copy configs (measured, warmed clock:
+    // 2048^3 130.2 -> 128.5 us, 1023^3 24.0 -> 23.4 us; the same at the
+    // 16-byte 64x64 tile made 1000^3 and 1024^3 1-2% slower).
+    constexpr int kHintReads = FM + 2 * FN + ((FN == 1 && (BM == 128 || Cfg::CW == 1)) ? 1 : 0);
     // With ILV the scheduler is asked to spread the LDS reads of the next
     // group between this group's MFMAs (two MFMAs, one read, ...).
     auto interleave_hint = [&]() {
         if (Cfg::ILV) {
-            constexpr int kReads = FM + 2 * FN;  // b128 A reads + paired b32 B reads
+            constexpr int kReads = kHintReads;
             constexpr int kMfma = 4 * FM * FN;
             constexpr int kPer = kMfma >= 2 * kReads ? 2 : 1;
             constexpr int kPairs = kMfma / kPer < kReads ? kMfma / kPer : kReads;
@@ -914,7 +920,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
     auto interleave_hint_copies = [&]() {
         if (Cfg::ILV) {
             constexpr int kMfma = 4 * FM * FN;
-            spread_hint<kMfma, FM + 2 * FN, PER_TILE>(std::make_integer_sequence<int, kMfma>{});
+            spread_hint<kMfma, kHintReads, PER_TILE>(std::make_integer_sequence<int, kMfma>{});
         }
     };
 
