@@ -684,16 +684,27 @@ struct DmaOperand {
     // A tile wholly inside K: no per-copy bounds work.
     __device__ __forceinline__ void issue_full(const float* __restrict__ base, int64_t ld, int k0,
                                                float* stage) const {
-        const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
-        if constexpr (CW == 4) {
+        issue_part<0, PER>(base, ld, k0, stage);
+    }
+
+    // Copies I0 .. I1-1 of issue_full (a tile may be copied in parts).
+    template <int I0, int I1>
+    __device__ __forceinline__ void issue_part(const float* __restrict__ base, int64_t ld, int k0,
+                                               float* stage) const {
+        static_assert(0 <= I0 && I0 <= I1 && I1 <= PER, "a range of this tile's copies");
+        if constexpr (I0 < I1) {
+            const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
+            if constexpr (CW == 4) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i) copy(base + goff[i] + koff, stage + loff[i]);
-        } else {
-            // The tile's wave-uniform base in a buffer descriptor (scalar
-            // registers), each copy's lane part as a 32-bit offset from it.
-            const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
+                for (int i = I0; i < I1; ++i) copy(base + goff[i] + koff, stage + loff[i]);
+            } else {
+                // The tile's wave-uniform base in a buffer descriptor (scalar
+                // registers), each copy's lane part as a 32-bit offset from it.
+                const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
 #pragma unroll
-            for (int i = 0; i < PER; ++i) dma_buf_copy4(rsrc, (uint32_t)lo[i] * 4u, stage + loff[i]);
+                for (int i = I0; i < I1; ++i)
+                    dma_buf_copy4(rsrc, (uint32_t)lo[i] * 4u, stage + loff[i]);
+            }
         }
     }
 
@@ -731,6 +742,16 @@ struct DmaOperand {
     }
 };
 
+// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
+template <class F, int... G>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, G...>) {
+    (f(std::integral_constant<int, G>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Scheduling hint for one MFMA group: after MFMA j, the reads and copies
 // that bring the running totals to ceil(total * (j + 1) / kMfma), so both are
 // spread evenly over the group (the builtin needs constant counts).
@@ -746,6 +767,26 @@ __device__ __forceinline__ void spread_hint_one() {
 template <int kMfma, int kReads, int kCopies, int... J>
 __device__ __forceinline__ void spread_hint(std::integer_sequence<int, J...>) {
     (spread_hint_one<kMfma, kReads, kCopies, J>(), ...);
+}
+
+// The same for a group whose fragment reads come before its copies in
+// program order (the copies write LDS, so the compiler keeps every read
+// ahead of them): the reads spread over the first kSpan MFMAs, the copies
+// over the rest.
+template <int kMfma, int kReads, int kCopies, int kSpan, int J>
+__device__ __forceinline__ void front_hint_one() {
+    static_assert(kSpan > 0 && kSpan < kMfma, "reads and copies each get some MFMAs");
+    constexpr int M2 = kMfma - kSpan, J2 = J - kSpan;
+    constexpr int r = J < kSpan ? (kReads * (J + 1) + kSpan - 1) / kSpan - (kReads * J + kSpan - 1) / kSpan : 0;
+    constexpr int c = J >= kSpan ? (kCopies * (J2 + 1) + M2 - 1) / M2 - (kCopies * J2 + M2 - 1) / M2 : 0;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);  // DS reads
+    if constexpr (c > 0) __builtin_amdgcn_sched_group_barrier(0x010, c, 0);  // VMEM
+}
+
+template <int kMfma, int kReads, int kCopies, int kSpan, int... J>
+__device__ __forceinline__ void front_hint(std::integer_sequence<int, J...>) {
+    (front_hint_one<kMfma, kReads, kCopies, kSpan, J>(), ...);
 }
 
 // Block -> (batch, tile) for a launch whose 1-D grid covers every tile of
@@ -925,17 +966,29 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
     };
 
     if constexpr (Cfg::XPIPE != 0) {
-        // Cross-tile pipeline (two stages): the barrier sits before the last
-        // group's MFMAs, so the first reads of tile t+1 are in flight while
-        // those MFMAs run.  At the barrier every wave has read all of tile t
-        // (lgkmcnt 0) and tile t+1 has landed (vmcnt 0: it is the only copy in
-        // flight), so tile t+2 can go into tile t's stage right after it.
-        static_assert(S == 2 && NGK % 2 == 0, "cross-tile pipeline: 2 stages, even group count");
+        // Cross-tile pipeline: the barrier sits before the last group's
+        // MFMAs, so the first reads of tile t+1 are in flight while those
+        // MFMAs run.  The last group's fragments are read before the barrier,
+        // so at the barrier every wave has read all of tile t (lgkmcnt 0) and
+        // tile t+1 has landed.
+        // S = 2: tile t's stage is then free, and tile t+2 goes into it in
+        // the group after the barrier (the copies share that group's MFMAs).
+        // S = 3: tile t+2 goes into tile t-1's stage, free since the previous
+        // barrier, so its copies are spread over all of tile t's groups
+        // (chunk g in group g).  The barrier then waits for tile t+1 only,
+        // with the chunks of tile t+2 issued before it still in flight.
+        static_assert((S == 2 || S == 3) && NGK % 2 == 0,
+                      "cross-tile pipeline: 2 or 3 stages, even group count");
         using No = std::false_type;
         using Yes = std::true_type;
+        // Copies of chunk g of a tile: [chunk_lo(g), chunk_lo(g + 1)) of the
+        // tile's PER_TILE copies (A's, then B's).
+        constexpr auto chunk_lo = [](int g) { return g * PER_TILE / NGK; };
+        constexpr int kPre = S == 3 ? chunk_lo(NGK - 1) : 0;  // copies issued before the barrier
         const bool has_tail = tail_tile >= 0;
+        // Tiles 0 .. S-2 are in flight; with S = 2 add tile 1; wait for tile 0.
+        if (S == 2 && ktiles > 1) issue_tile(1, 1);
         if (ktiles > 1) {
-            issue_tile(1, 1);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_TILE));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -948,39 +1001,80 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         } else {
             read_group(As, Bs, g0, 0, 0, No{});
         }
+        // Stage of tile t is t % S; `cur` carries it (no division in the loop).
+        auto next_stage = [](int c) { return c + 1 == S ? 0 : c + 1; };
+        auto copy_chunk = [&](auto gc, int k0, int dst) __attribute__((always_inline)) {
+            constexpr int c0 = chunk_lo(decltype(gc)::value);
+            constexpr int c1 = chunk_lo(decltype(gc)::value + 1);
+            constexpr int PA = OpA::PER;
+            opa.template issue_part<(c0 < PA ? c0 : PA), (c1 < PA ? c1 : PA)>(
+                A, p.lda, k0, As + dst * OpA::STAGE);
+            opb.template issue_part<(c0 > PA ? c0 - PA : 0), (c1 > PA ? c1 - PA : 0)>(
+                B, p.ldb, k0, Bs + dst * OpB::STAGE);
+        };
+        // Scheduling hint of group g with S = 3: the next group's reads, then
+        // chunk g's copies.
+        auto chunk_hint = [&](auto gc) __attribute__((always_inline)) {
+            if (Cfg::ILV) {
+                constexpr int kMfma = 4 * FM * FN;
+                constexpr int kCopies = chunk_lo(decltype(gc)::value + 1) - chunk_lo(decltype(gc)::value);
+                if constexpr (kCopies == 0) {
+                    interleave_hint();
+                } else {
+                    front_hint<kMfma, kHintReads, kCopies, kMfma / 2>(
+                        std::make_integer_sequence<int, kMfma>{});
+                }
+            }
+        };
         // One K-tile of the steady state (tiles t+1 and t+2 exist and are
         // wholly inside K).  Nothing here branches, so each group's fragment
         // reads stay in one scheduling region with the MFMAs they are
         // interleaved with.
-        auto ktile_steady = [&](int t) __attribute__((always_inline)) {
-            const int cur = t & 1;
+        auto ktile_steady = [&](int t, int cur) __attribute__((always_inline)) {
+            const int nxt = next_stage(cur);
+            const int dst = S == 2 ? cur : next_stage(nxt);  // tile t+2's stage
             const float* as = As + cur * OpA::STAGE;
             const float* bs = Bs + cur * OpB::STAGE;
-#pragma unroll
-            for (int g = 0; g + 1 < NGK; ++g) {
+            static_for<NGK - 1>([&](auto gc) __attribute__((always_inline)) {
+                constexpr int g = decltype(gc)::value;
                 __builtin_amdgcn_sched_barrier(0);
                 read_group(as, bs, g0 + g + 1, (g + 1) & 1, t, No{});
+                if constexpr (S == 3) copy_chunk(gc, (t + 2) * BK, dst);
                 mfma_group(g & 1);
-                interleave_hint();
+                if constexpr (S == 3) {
+                    chunk_hint(gc);
+                } else {
+                    interleave_hint();
+                }
                 __builtin_amdgcn_sched_barrier(0);
-            }
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // vmcnt(0) lgkmcnt(0)
+            });
+            // lgkmcnt(0), and tile t+1 landed (only tile t+2's copies issued
+            // above may still be in flight)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPre) & ~(15 << 8));
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
-            // The copies of tile t+2 (into the stage every wave has finished
-            // reading) and the first reads of tile t+1 are spread between the
-            // last group's MFMAs.
-            opa.issue_full(A, p.lda, (t + 2) * BK, As + cur * OpA::STAGE);
-            opb.issue_full(B, p.ldb, (t + 2) * BK, Bs + cur * OpB::STAGE);
-            read_group(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, g0, 0, t + 1, No{});
-            mfma_group((NGK - 1) & 1);
-            interleave_hint_copies();
+            if constexpr (S == 2) {
+                // The copies of tile t+2 (into the stage every wave has
+                // finished reading) and the first reads of tile t+1 are
+                // spread between the last group's MFMAs.
+                opa.issue_full(A, p.lda, (t + 2) * BK, As + dst * OpA::STAGE);
+                opb.issue_full(B, p.ldb, (t + 2) * BK, Bs + dst * OpB::STAGE);
+                read_group(As + nxt * OpA::STAGE, Bs + nxt * OpB::STAGE, g0, 0, t + 1, No{});
+                mfma_group((NGK - 1) & 1);
+                interleave_hint_copies();
+            } else {
+                read_group(As + nxt * OpA::STAGE, Bs + nxt * OpB::STAGE, g0, 0, t + 1, No{});
+                copy_chunk(std::integral_constant<int, NGK - 1>{}, (t + 2) * BK, dst);
+                mfma_group((NGK - 1) & 1);
+                chunk_hint(std::integral_constant<int, NGK - 1>{});
+            }
             __builtin_amdgcn_sched_barrier(0);
         };
         // The last tiles (up to three), with run-time checks for the tile
-        // that crosses K and for the end of K.
+        // that crosses K and for the end of K; tile t+2 is copied whole
+        // after the barrier.
         auto read_rt = [&](const float* as, const float* bs, int g, int slot, int tile) {
             if (tile == tail_tile) {
                 read_group(as, bs, g, slot, tile, Yes{});
@@ -988,8 +1082,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                 read_group(as, bs, g, slot, tile, No{});
             }
         };
-        auto ktile_last = [&](int t) {
-            const int cur = t & 1;
+        auto ktile_last = [&](int t, int cur) {
+            const int nxt = next_stage(cur);
+            const int dst = S == 2 ? cur : next_stage(nxt);
             const float* as = As + cur * OpA::STAGE;
             const float* bs = Bs + cur * OpB::STAGE;
 #pragma unroll
@@ -1004,10 +1099,10 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (t + 2 < ktiles) issue_tile(t + 2, cur);
+            if (t + 2 < ktiles) issue_tile(t + 2, dst);
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < ktiles) {
-                read_rt(As + (cur ^ 1) * OpA::STAGE, Bs + (cur ^ 1) * OpB::STAGE, g0, 0, t + 1);
+                read_rt(As + nxt * OpA::STAGE, Bs + nxt * OpB::STAGE, g0, 0, t + 1);
             }
             mfma_group((NGK - 1) & 1);
             interleave_hint();
@@ -1017,8 +1112,15 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         // a full tile needs no checks until its last two tiles.
         const int steady = has_tail ? ktiles - 3 : ktiles - 2;
         int t = 0;
-        for (; t < steady; ++t) ktile_steady(t);
-        for (; t < ktiles; ++t) ktile_last(t);
+        int cur = 0;
+        for (; t < steady; ++t) {
+            ktile_steady(t, cur);
+            cur = next_stage(cur);
+        }
+        for (; t < ktiles; ++t) {
+            ktile_last(t, cur);
+            cur = next_stage(cur);
+        }
     } else {
         int stage = 0;
         for (int t = 0; t < ktiles; ++t) {
@@ -1738,6 +1840,19 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
     return hipGetLastError();
 }
 
+// Launches the three-stage config One when the grid has at most one block
+// per CU (256 CUs), else the two-stage Two, whose 64 KB of LDS lets two
+// blocks share a CU.
+template <class One, class Two>
+hipError_t launch_dma_fit(const GemmParams& p, bool ta, bool tb, int nbatch, hipStream_t stream) {
+    static_assert(One::BM == Two::BM && One::BN == Two::BN, "twins with the same tile");
+    constexpr int64_t kCUs = 256;
+    const int64_t blocks =
+        (int64_t)((p.M + One::BM - 1) / One::BM) * ((p.N + One::BN - 1) / One::BN) * nbatch;
+    return blocks <= kCUs ? launch_dma<One>(p, ta, tb, nbatch, stream)
+                          : launch_dma<Two>(p, ta, tb, nbatch, stream);
+}
+
 template <int KW, int ITS = 4>
 hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                               int nbatch, hipStream_t stream) {
@@ -2012,6 +2127,10 @@ using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
 // still runs two waves per SIMD (1024^3: 24.3 vs 25.9 us with one set, and
 // 42 us for the split-K kernel).
 using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2>;
+// Its three-stage twin, for grids of at most one block per CU: each tile's
+// copies are spread over all four of its k-groups instead of the one after
+// the barrier (96 KB of LDS, so one block per CU).
+using CfgDma64S3 = DmaCfg<64, 64, 64, 32, 32, 3, 1, 1, 2>;
 // 128x128x64 with eight waves of 64x32 and 128 KB of LDS (one block per CU):
 // two waves per SIMD where the GPU holds about one 128x128 tile per CU
 // (2048^3: 131 vs 136.5 us for Dma128 in the same run).
@@ -2020,6 +2139,7 @@ using CfgDma128W8 = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1>;
 // 4-byte-aligned pointer, at 2-3% below their 16-byte twins (1023^3: 26.5 us
 // against 44 us for split-K; 4095^3: 1.11 ms).
 using CfgDma64U = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2, 1>;
+using CfgDma64US3 = DmaCfg<64, 64, 64, 32, 32, 3, 1, 1, 2, 1>;  // 1023^3: 24.1 -> 23.5 us
 // 64x64x16 with four stages: every 16-deep K-tile of a short-K problem is
 // copied at once and each is multiplied as soon as it lands, so a block's
 // MFMAs overlap the arrival of its later tiles (the C4 batch, K = 64).
@@ -2028,8 +2148,10 @@ using CfgDma64S = DmaCfg<64, 64, 16, 32, 32, 4, 0, 1>;
 // (twelve waves, three per SIMD): three quarters of a 64x64 tile's work, for
 // problems whose 64x64 tiles leave many CUs idle (777^3: 225 tiles instead
 // of 169 on 256 CUs).  Its 32-wide operand's 2048 copy units do not divide
-// over the 768 lanes; the surplus copies repeat the stage's last one.
-using CfgDma96x32U = DmaCfg<96, 32, 64, 32, 32, 2, 1, 1, 4, 1>;
+// over the 768 lanes; the surplus copies repeat the stage's last one.  Three
+// stages, so each tile's eleven copies per lane are spread over both of its
+// k-groups (777^3: 18.1 -> 17.4 us).
+using CfgDma96x32U = DmaCfg<96, 32, 64, 32, 32, 3, 1, 1, 4, 1>;
 using CfgDma128W8U = DmaCfg<128, 128, 64, 64, 32, 2, 1, 1, 1, 1>;
 
 // Dispatch cost model.  A config runs `slots` blocks per CU at full
@@ -2392,13 +2514,13 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 err = launch_dma<CfgDma128>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma64:
-                err = launch_dma<CfgDma64>(p, transA, transB, nb, stream);
+                err = launch_dma_fit<CfgDma64S3, CfgDma64>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma128W8:
                 err = launch_dma<CfgDma128W8>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma64U:
-                err = launch_dma<CfgDma64U>(p, transA, transB, nb, stream);
+                err = launch_dma_fit<CfgDma64US3, CfgDma64U>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma128W8U:
                 err = launch_dma<CfgDma128W8U>(p, transA, transB, nb, stream);

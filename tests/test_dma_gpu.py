@@ -23,8 +23,10 @@ DMAS = DMAS16 + [(capi.KERNEL_DMA64U, 64), (capi.KERNEL_DMA128W8U, 64),
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
 # M and N multiples of 4 (either may be the contiguous extent), ragged against
 # the tiles; K in K-tiles (16 or 32 each) covering 1, 2, 3 and many K-tiles.
+# (1088, 1040) is 289 blocks of 64x64: more than one per CU, so the 64x64
+# configs take their two-stage form there and the three-stage one elsewhere.
 SHAPES = [(4, 4, 1), (256, 256, 2), (260, 300, 3), (516, 260, 17), (64, 1000, 6),
-          (768, 512, 64)]
+          (768, 512, 64), (1088, 1040, 5)]
 
 
 def _rng(*key):
