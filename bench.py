@@ -683,7 +683,7 @@ def main():
                "graph_steps_per_s": graph_sps, "graph_ms_per_step": graph_ms,
                "final_loss": loss,
                "config": "784-256-10, batch 256, lr 0.1, full step (forward, softmax-CE, "
-                         "backward incl. dX, SGD): one fdl_mlp2_train_step call (4 launches) "
+                         "backward incl. dX, SGD): one fdl_mlp2_train_step call (3 launches) "
                          "per step; graph = the same step replayed as a HIP graph"}
     idx = None
     if not args.no_mlp:
