@@ -10,6 +10,7 @@
 //   result   : lane l, register r holds D[i][j] with j = l % 32 and
 //              i = 8 * (r / 4) + 4 * (l / 32) + (r % 4)
 #include "fdl_device.hpp"
+#include "dma256_loop.inc"
 #include "fdl_internal.hpp"
 
 #include <algorithm>
@@ -513,9 +514,12 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // sums are added in set order after the K loop.
 // CW is the copy width in floats per lane (4: 16-byte copies, which need
 // 16-byte-aligned operand rows and K % 4 == 0; 1: 4-byte copies, any shape).
+// ASM = 1: the steady-state K loop is the hand-scheduled one of
+// dma256_loop.inc (only CfgDma256W4 on NN problems; see its generator).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
-          int ILV_ = 0, int KS_ = 1, int CW_ = 4, int WPE_ = 1>
+          int ILV_ = 0, int KS_ = 1, int CW_ = 4, int WPE_ = 1, int ASM_ = 0>
 struct DmaCfg {
+    static constexpr int ASM = ASM_;
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int STAGES = STAGES_;
     static constexpr int XPIPE = XPIPE_, ILV = ILV_, KS = KS_, CW = CW_;
@@ -996,10 +1000,85 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (tail_tile == 0) {
-            read_group(As, Bs, g0, 0, 0, Yes{});
+        int t = 0;  // the next K-tile the C++ loops below run
+        if constexpr (Cfg::ASM != 0) {
+            static_assert(!TA && !TB && S == 3 && BM == 256 && BN == 256 && BK == 16 &&
+                              FM == 4 && FN == 4 && KS == 1 && Cfg::CW == 4 && NT == 256,
+                          "the hand-scheduled loop is written for CfgDma256W4 on NN problems");
+            // Whole groups of three steady K-tiles (tile t+2 full and inside
+            // K) run in the asm loop; it starts where this code stands (tiles
+            // 0 and 1 issued, tile 0 landed) and leaves the C++ loops the same
+            // state at tile 3 * cnt, stage 0: group 0 of that tile is read
+            // again below, tile 3 * cnt + 1 is in flight.
+            int cnt = (has_tail ? ktiles - 3 : ktiles - 2) / 3;
+            if (cnt > 0) {
+                t = 3 * cnt;
+                auto uniform = [](const float* q) {
+                    const uint64_t v = (uint64_t)q;
+                    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+                    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+                    return (const float*)(lo | (hi << 32));
+                };
+                // Copies: each operand's base in a buffer descriptor, the lane
+                // offsets of the wave's four copies, the K-tile's offset in a
+                // scalar (tile 2 first); the host keeps every offset below 2^31.
+                const __amdgpu_buffer_rsrc_t rsa = dma_buffer(uniform(A));
+                const __amdgpu_buffer_rsrc_t rsb = dma_buffer(uniform(B));
+                const uint32_t va0 = (uint32_t)(opa.goff[0] * 4), va1 = (uint32_t)(opa.goff[1] * 4),
+                               va2 = (uint32_t)(opa.goff[2] * 4), va3 = (uint32_t)(opa.goff[3] * 4);
+                const uint32_t vb0 = (uint32_t)(opb.goff[0] * 4), vb1 = (uint32_t)(opb.goff[1] * 4),
+                               vb2 = (uint32_t)(opb.goff[2] * 4), vb3 = (uint32_t)(opb.goff[3] * 4);
+                uint32_t soa = 2 * BK * 4;
+                uint32_t sob = __builtin_amdgcn_readfirstlane((uint32_t)(2 * BK * p.ldb * 4));
+                const uint32_t bstep = __builtin_amdgcn_readfirstlane((uint32_t)(BK * p.ldb * 4));
+                // LDS byte addresses: each copy's wave base (M0, before the
+                // stage offset) and the lanes' fragment read bases.
+                const uint32_t lds_a = (uint32_t)(uintptr_t)As;
+                const uint32_t lds_b = (uint32_t)(uintptr_t)Bs;
+                const uint32_t ma0 = __builtin_amdgcn_readfirstlane(lds_a + opa.loff[0] * 4);
+                const uint32_t ma1 = __builtin_amdgcn_readfirstlane(lds_a + opa.loff[1] * 4);
+                const uint32_t ma2 = __builtin_amdgcn_readfirstlane(lds_a + opa.loff[2] * 4);
+                const uint32_t ma3 = __builtin_amdgcn_readfirstlane(lds_a + opa.loff[3] * 4);
+                const uint32_t mb0 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[0] * 4);
+                const uint32_t mb1 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[1] * 4);
+                const uint32_t mb2 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[2] * 4);
+                const uint32_t mb3 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[3] * 4);
+                const int row = wm0 + l32;  // as OpA::read: 16-byte k-chunk (2g + half) rotated
+                const uint32_t ra0 = lds_a + row * 64 + 16 * ((0 + half) ^ kc_swz<OpA::CPR>(row));
+                const uint32_t ra1 = lds_a + row * 64 + 16 * ((2 + half) ^ kc_swz<OpA::CPR>(row));
+                const uint32_t rbl = lds_b + (4 * half * BN + wn0 + l32) * 4;  // as OpB::read
+                const uint32_t rb0 = rbl, rb1 = rbl + 128, rb2 = rbl + 256, rb3 = rbl + 384;
+                int m0s;
+                asm volatile(FDL_DMA256W4_LOOP
+                    : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c02] "+a"(acc[0][2]),
+                      [c03] "+a"(acc[0][3]), [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]),
+                      [c12] "+a"(acc[1][2]), [c13] "+a"(acc[1][3]), [c20] "+a"(acc[2][0]),
+                      [c21] "+a"(acc[2][1]), [c22] "+a"(acc[2][2]), [c23] "+a"(acc[2][3]),
+                      [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]), [c32] "+a"(acc[3][2]),
+                      [c33] "+a"(acc[3][3]),
+                      [cnt] "+s"(cnt), [m0s] "=&s"(m0s), [soa] "+s"(soa), [sob] "+s"(sob)
+                    : [ma0] "s"(ma0), [ma1] "s"(ma1), [ma2] "s"(ma2), [ma3] "s"(ma3),
+                      [mb0] "s"(mb0), [mb1] "s"(mb1), [mb2] "s"(mb2), [mb3] "s"(mb3),
+                      [bstep] "s"(bstep), [rsa] "s"(rsa), [rsb] "s"(rsb),
+                      [va0] "v"(va0), [va1] "v"(va1), [va2] "v"(va2), [va3] "v"(va3),
+                      [vb0] "v"(vb0), [vb1] "v"(vb1), [vb2] "v"(vb2), [vb3] "v"(vb3),
+                      [ra0] "v"(ra0), [ra1] "v"(ra1),
+                      [rb0] "v"(rb0), [rb1] "v"(rb1), [rb2] "v"(rb2), [rb3] "v"(rb3)
+                    : "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168",
+                      "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177",
+                      "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186",
+                      "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195",
+                      "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204",
+                      "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213",
+                      "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222",
+                      "v223", "scc", "memory");
+            }
+        }
+        // Group 0 of tile t (stage 0: t is 0 or a multiple of 3).
+        if (tail_tile == t) {
+            read_group(As, Bs, g0, 0, t, Yes{});
         } else {
-            read_group(As, Bs, g0, 0, 0, No{});
+            read_group(As, Bs, g0, 0, t, No{});
         }
         // Stage of tile t is t % S; `cur` carries it (no division in the loop).
         auto next_stage = [](int c) { return c + 1 == S ? 0 : c + 1; };
@@ -1111,7 +1190,6 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         // Steady state while tile t+2 is not the last tile; a K that ends in
         // a full tile needs no checks until its last two tiles.
         const int steady = has_tail ? ktiles - 3 : ktiles - 2;
-        int t = 0;
         int cur = 0;
         for (; t < steady; ++t) {
             ktile_steady(t, cur);
@@ -1824,7 +1902,11 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
     const int flat = nbatch > 1 && tiles <= kFlatBatchMaxTiles;
     const dim3 grid = flat ? dim3(tiles * nbatch) : dim3(tiles, nbatch);
     const dim3 block(Cfg::NT);
-    if (!ta && !tb) {
+    if constexpr (Cfg::ASM != 0) {  // the hand-scheduled loop exists for NN only
+        if (ta || tb) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
+                           tiles_m, tiles_n, flat);
+    } else if (!ta && !tb) {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
                            tiles_m, tiles_n, flat);
     } else if (!ta) {
@@ -1838,6 +1920,16 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
                            tiles_m, tiles_n, flat);
     }
     return hipGetLastError();
+}
+
+// Whether CfgDma256W4 runs this Dma256 problem: NN, K of at least 16
+// K-tiles, and each operand's extent (one batch) below 2 GiB, so the loop's
+// 32-bit buffer offsets (lane part plus K-tile part) cannot wrap.
+bool dma256w4_ok(const GemmParams& p, bool ta, bool tb) {
+    constexpr int64_t kLimit = int64_t(1) << 31;
+    const int64_t a_bytes = ((int64_t)(p.M - 1) * p.lda + p.K) * 4;
+    const int64_t b_bytes = ((int64_t)(p.K - 1) * p.ldb + p.N) * 4;
+    return !ta && !tb && p.K >= 256 && a_bytes < kLimit && b_bytes < kLimit;
 }
 
 // Launches the three-stage config One when the grid has at most one block
@@ -2121,6 +2213,13 @@ using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
 // tiles would leave CUs idle (2048^3: 0.161 vs 0.178 ms for Tiled128W8;
 // 4000x3000x2048: 0.45 vs 0.54 ms for the 256x256 tile).
 using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
+// The same tile as four waves of 128x128 (one per SIMD, 256 accumulators in
+// AGPRs) with three stages and the hand-scheduled steady-state loop of
+// dma256_loop.inc: NN problems with K >= 256 whose operands span less than
+// 2 GiB (the loop's copies use 32-bit buffer offsets).  4096^3: 945 -> 915-920
+// us; results bit-identical to CfgDma256 (each output adds the same products
+// in the same order).
+using CfgDma256W4 = DmaCfg<256, 256, 16, 128, 128, 3, 1, 1, 1, 4, 1, 1>;
 using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
 // 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU.  Two
 // sets of four 32x32 waves split each K-tile's k-groups, so one block per CU
@@ -2508,7 +2607,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             }
             case GemmKernel::Dma256:
-                err = launch_dma<CfgDma256>(p, transA, transB, nb, stream);
+                err = dma256w4_ok(p, transA, transB)
+                          ? launch_dma<CfgDma256W4>(p, transA, transB, nb, stream)
+                          : launch_dma<CfgDma256>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma128:
                 err = launch_dma<CfgDma128>(p, transA, transB, nb, stream);
