@@ -1,0 +1,217 @@
+"""Writes dma_loops.inc: the hand-scheduled steady-state K loops of the
+four-wave direct-to-LDS tiles of sgemm.hip, one inline-asm statement each.
+
+    python fast_dl_amd/csrc/gen_dma_loops.py fast_dl_amd/csrc/dma_loops.inc
+
+Each loop is the compiler-scheduled XPIPE loop of sgemm_dma_kernel with three
+LDS stages, NN layout, written out instruction by instruction so that every
+MFMA, fragment read, copy and wait sits where it is placed here:
+
+  * four waves, one per SIMD, each owning a WM x WN block of the tile as
+    FM x FN accumulators of 32x32 (AGPRs, operands %[c<mi><ni>]);
+  * a K-tile is NG k-groups of 8; each group is 4*FM*FN
+    v_mfma_f32_32x32x2_f32 in the order (q, mi, ni), so an accumulator is
+    reused every FM*FN MFMAs;
+  * during group g the wave reads group g+1's fragments (the last group reads
+    group 0 of tile t+1) into the other register slot and issues chunk g of
+    tile t+2's copies (A's copies first, then B's, spread over the groups as
+    sgemm_dma_kernel's three-stage form does); the barrier sits before the
+    last group, after a wait for tile t+1 (vmcnt: only tile t+2's chunks
+    issued so far may still be in flight) and for the reads;
+  * copies are buffer_load_dwordx4 ... lds: the operand's base in a buffer
+    descriptor, a 32-bit lane offset per copy, the K-tile's offset in one
+    scalar register advanced once per tile (no per-copy address arithmetic);
+  * the stages rotate with the K-tile, so the loop body is three K-tiles long
+    and every LDS offset is an immediate.
+
+Fragments live in fixed registers from v160 (clobbered by the statement):
+slot s, A block mi: 4 registers (one ds_read_b128: the four k values of a
+lane's row in the group); B block ni: 4 registers (two ds_read2st64_b32: k
+rows BN floats apart).  Measured on MI355X at 4096^3 (256x256 tile): 945 us
+for the compiler-scheduled eight-wave tile, 930 us for this loop with
+global_load_lds copies, 911-920 us with buffer copies.
+"""
+import sys
+from dataclasses import dataclass
+
+
+@dataclass
+class Loop:
+    macro: str
+    bm: int
+    bn: int
+    bk: int
+    wm: int
+    wn: int
+    read_every: int       # MFMAs between two fragment reads
+    copy_slots: tuple     # MFMAs of a group after which its copies go
+    nt: int = 256
+    stages: int = 3
+
+    @property
+    def fm(self):
+        return self.wm // 32
+
+    @property
+    def fn(self):
+        return self.wn // 32
+
+    @property
+    def ng(self):
+        return self.bk // 8
+
+    @property
+    def stage_a(self):
+        return self.bm * self.bk * 4
+
+    @property
+    def stage_b(self):
+        return self.bk * self.bn * 4
+
+    @property
+    def per_a(self):
+        return self.bm * self.bk // 4 // self.nt
+
+    @property
+    def per_b(self):
+        return self.bk * self.bn // 4 // self.nt
+
+    def a_base_per_mi(self):
+        """Whether a lane's rotated k-chunk differs between its A blocks (the
+        rotation of a k-contiguous row r is kc_swz(r); blocks are 32 rows apart)."""
+        cpr = self.bk // 4
+        swz = {4: lambda r: (r >> 2) & 3, 8: lambda r: (r ^ (r >> 3)) & 7, 16: lambda r: r & 15}[cpr]
+        return any(swz(r) != swz(r + 32 * mi) for r in range(64) for mi in range(self.fm))
+
+
+def emit(L: Loop) -> list:
+    fm, fn, ng = L.fm, L.fn, L.ng
+    slot_regs = 4 * (fm + fn)
+    assert 160 + 2 * slot_regs <= 256
+    per_tile = L.per_a + L.per_b
+    per_mi = L.a_base_per_mi()
+
+    def areg(s, mi):
+        return 160 + slot_regs * s + 4 * mi
+
+    def breg(s, ni):
+        return 160 + slot_regs * s + 4 * fm + 4 * ni
+
+    def reads(slot, g, stage):
+        out = []
+        for mi in range(fm):
+            r = areg(slot, mi)
+            if per_mi:   # %[ra<g><mi>]: the lane's row start plus its rotated k-chunk
+                out.append(f"ds_read_b128 v[{r}:{r + 3}], %[ra{g}{mi}] offset:{stage * L.stage_a}")
+            else:        # %[ra<g>]: the same for block 0; blocks are 32 rows apart
+                out.append(f"ds_read_b128 v[{r}:{r + 3}], %[ra{g}] "
+                           f"offset:{stage * L.stage_a + mi * 32 * L.bk * 4}")
+        row_units = L.bn * 4 // 256   # one k row of B, in ds_read2st64's 256-byte units
+        for ni in range(fn):
+            r = breg(slot, ni)
+            for p in range(2):
+                # %[rb<ni>]: the lane's column and k half
+                o0 = stage * L.stage_b // 256 + (8 * g + 2 * p) * row_units
+                assert o0 + row_units <= 255
+                out.append(f"ds_read2st64_b32 v[{r + 2 * p}:{r + 2 * p + 1}], %[rb{ni}] "
+                           f"offset0:{o0} offset1:{o0 + row_units}")
+        return out
+
+    def chunk_lo(g):
+        return g * per_tile // ng
+
+    def copy(i, stage):
+        op, j = ("a", i) if i < L.per_a else ("b", i - L.per_a)
+        base = L.stage_a if op == "a" else L.stage_b
+        return [f"s_add_u32 m0, %[m{op}{j}], {stage * base}",
+                "s_nop 0",   # M0 written by SALU, then read by an LDS DMA: one wait state
+                f"buffer_load_dwordx4 %[v{op}{j}], %[rs{op}], %[so{op}] offen lds"]
+
+    def advance(op):
+        return f"s_add_u32 %[so{op}], %[so{op}], {L.bk * 4 if op == 'a' else '%[bstep]'}"
+
+    def group(slot, rd, cps, advances):
+        out = []
+        rd = list(rd)
+        n = 4 * fm * fn
+        slots = [1 + L.read_every * i for i in range(len(rd))]
+        assert slots[-1] < n
+        last_copy = max(L.copy_slots[:len(cps)]) if cps else -1
+        for j in range(n):
+            q, mi, ni = j // (fm * fn), (j // fn) % fm, j % fn
+            out.append(f"v_mfma_f32_32x32x2_f32 %[c{mi}{ni}], v{areg(slot, mi) + q}, "
+                       f"v{breg(slot, ni) + q}, %[c{mi}{ni}]")
+            if j in slots:
+                out.append(rd.pop(0))
+            for k, cj in enumerate(L.copy_slots[:len(cps)]):
+                if cj == j:
+                    out += cps[k]
+            if j == last_copy + 2:   # two MFMAs after the last copy that reads the offset
+                out += advances
+        assert not rd
+        return out
+
+    def ktile(phase):
+        cur, nxt, dst = phase, (phase + 1) % 3, (phase + 2) % 3   # stages of tiles t, t+1, t+2
+        out = ["s_waitcnt lgkmcnt(0)"]                            # slot 0: group 0 of tile t
+        for g in range(ng):
+            slot = g & 1
+            if g + 1 < ng:
+                rd = reads(slot ^ 1, g + 1, cur)
+            else:
+                rd = reads(slot ^ 1, 0, nxt)
+                out += [f"s_waitcnt vmcnt({chunk_lo(ng - 1)}) lgkmcnt(0)", "s_barrier"]
+            ids = range(chunk_lo(g), chunk_lo(g + 1))
+            cps = [copy(i, dst) for i in ids]
+            advances = []
+            if L.per_a - 1 in ids:
+                advances.append(advance("a"))
+            if per_tile - 1 in ids:
+                advances.append(advance("b"))
+            out += group(slot, rd, cps, advances)
+            if g + 2 < ng:
+                out.append("s_waitcnt lgkmcnt(0)")   # the next group's fragments
+        return out
+
+    lines = ["s_mov_b32 %[m0s], m0",   # M0 is the compiler's: saved and restored
+             "s_waitcnt lgkmcnt(0)",
+             "s_nop 4"]                # accumulators written just before by VALU
+    lines += reads(0, 0, 0)            # group 0 of tile 0
+    label = f"L_{L.macro.lower()}_%="
+    lines.append(f"{label}:")
+    for phase in range(3):
+        lines += ktile(phase)
+    lines += ["s_sub_u32 %[cnt], %[cnt], 1",
+              "s_cmp_lg_u32 %[cnt], 0",
+              f"s_cbranch_scc1 {label}",
+              "s_waitcnt lgkmcnt(0)",  # no read may land after the statement
+              "s_nop 7", "s_nop 7", "s_nop 7",  # last MFMAs retire before the compiler reads AGPRs
+              "s_mov_b32 m0, %[m0s]"]
+    out = [f"#define {L.macro} \\"]
+    out += [f'    "{line}\\n\\t" \\' for line in lines]
+    out.append('    ""')
+    return out
+
+
+LOOPS = [
+    # 256x256x16, waves of 128x128 (CfgDma256W4): a read every 5 MFMAs from
+    # the second, a group's four copies after its first four MFMAs.
+    Loop("FDL_DMA256W4_LOOP", 256, 256, 16, 128, 128, read_every=5, copy_slots=(1, 2, 3, 4)),
+    # 128x128x32, waves of 64x64 (CfgDma128W4): four groups of 16 MFMAs, a
+    # read every 2 MFMAs, a group's two copies after its first two MFMAs.
+    Loop("FDL_DMA128W4_LOOP", 128, 128, 32, 64, 64, read_every=2, copy_slots=(1, 2)),
+]
+
+
+def main(path):
+    out = ["// Generated by gen_dma_loops.py (same directory); edit that, not this.",
+           "// Hand-scheduled steady-state K loops of the four-wave direct-to-LDS tiles.",
+           "#pragma once"]
+    for L in LOOPS:
+        out += [""] + emit(L)
+    with open(path, "w") as f:
+        f.write("\n".join(out) + "\n")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1])

@@ -10,7 +10,7 @@
 //   result   : lane l, register r holds D[i][j] with j = l % 32 and
 //              i = 8 * (r / 4) + 4 * (l / 32) + (r % 4)
 #include "fdl_device.hpp"
-#include "dma256_loop.inc"
+#include "dma_loops.inc"
 #include "fdl_internal.hpp"
 
 #include <algorithm>
@@ -514,8 +514,8 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // sums are added in set order after the K loop.
 // CW is the copy width in floats per lane (4: 16-byte copies, which need
 // 16-byte-aligned operand rows and K % 4 == 0; 1: 4-byte copies, any shape).
-// ASM = 1: the steady-state K loop is the hand-scheduled one of
-// dma256_loop.inc (only CfgDma256W4 on NN problems; see its generator).
+// ASM = 1: the steady-state K loop is a hand-scheduled one of dma_loops.inc
+// (CfgDma256W4 and CfgDma128W4 on NN problems; see its generator).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
           int ILV_ = 0, int KS_ = 1, int CW_ = 4, int WPE_ = 1, int ASM_ = 0>
 struct DmaCfg {
@@ -1002,9 +1002,12 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         asm volatile("" ::: "memory");
         int t = 0;  // the next K-tile the C++ loops below run
         if constexpr (Cfg::ASM != 0) {
-            static_assert(!TA && !TB && S == 3 && BM == 256 && BN == 256 && BK == 16 &&
-                              FM == 4 && FN == 4 && KS == 1 && Cfg::CW == 4 && NT == 256,
-                          "the hand-scheduled loop is written for CfgDma256W4 on NN problems");
+            static_assert(!TA && !TB && S == 3 && KS == 1 && Cfg::CW == 4 && NT == 256 &&
+                              ((BM == 256 && BN == 256 && BK == 16 && FM == 4 && FN == 4) ||
+                               (BM == 128 && BN == 128 && BK == 32 && FM == 2 && FN == 2)),
+                          "the hand-scheduled loops are written for CfgDma256W4 and CfgDma128W4 "
+                          "on NN problems");
+            static_assert(OpA::PER == 4 && OpB::PER == 4, "four copies of each operand per wave");
             // Whole groups of three steady K-tiles (tile t+2 full and inside
             // K) run in the asm loop; it starts where this code stands (tiles
             // 0 and 1 issued, tile 0 landed) and leaves the C++ loops the same
@@ -1043,35 +1046,59 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                 const uint32_t mb1 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[1] * 4);
                 const uint32_t mb2 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[2] * 4);
                 const uint32_t mb3 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[3] * 4);
-                const int row = wm0 + l32;  // as OpA::read: 16-byte k-chunk (2g + half) rotated
-                const uint32_t ra0 = lds_a + row * 64 + 16 * ((0 + half) ^ kc_swz<OpA::CPR>(row));
-                const uint32_t ra1 = lds_a + row * 64 + 16 * ((2 + half) ^ kc_swz<OpA::CPR>(row));
-                const uint32_t rbl = lds_b + (4 * half * BN + wn0 + l32) * 4;  // as OpB::read
-                const uint32_t rb0 = rbl, rb1 = rbl + 128, rb2 = rbl + 256, rb3 = rbl + 384;
+                // As OpA::read: row r's 16-byte k-chunk (2g + half) rotated by
+                // kc_swz(r); as OpB::read: column, k row 4 * half.
+                auto ra = [&](int g, int mi) {
+                    const int r = wm0 + mi * 32 + l32;
+                    return lds_a + r * BK * 4 + 16 * ((2 * g + half) ^ kc_swz<OpA::CPR>(r));
+                };
+                const uint32_t rbl = lds_b + (4 * half * BN + wn0 + l32) * 4;
                 int m0s;
-                asm volatile(FDL_DMA256W4_LOOP
-                    : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c02] "+a"(acc[0][2]),
-                      [c03] "+a"(acc[0][3]), [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]),
-                      [c12] "+a"(acc[1][2]), [c13] "+a"(acc[1][3]), [c20] "+a"(acc[2][0]),
-                      [c21] "+a"(acc[2][1]), [c22] "+a"(acc[2][2]), [c23] "+a"(acc[2][3]),
-                      [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]), [c32] "+a"(acc[3][2]),
-                      [c33] "+a"(acc[3][3]),
-                      [cnt] "+s"(cnt), [m0s] "=&s"(m0s), [soa] "+s"(soa), [sob] "+s"(sob)
-                    : [ma0] "s"(ma0), [ma1] "s"(ma1), [ma2] "s"(ma2), [ma3] "s"(ma3),
-                      [mb0] "s"(mb0), [mb1] "s"(mb1), [mb2] "s"(mb2), [mb3] "s"(mb3),
-                      [bstep] "s"(bstep), [rsa] "s"(rsa), [rsb] "s"(rsb),
-                      [va0] "v"(va0), [va1] "v"(va1), [va2] "v"(va2), [va3] "v"(va3),
-                      [vb0] "v"(vb0), [vb1] "v"(vb1), [vb2] "v"(vb2), [vb3] "v"(vb3),
-                      [ra0] "v"(ra0), [ra1] "v"(ra1),
-                      [rb0] "v"(rb0), [rb1] "v"(rb1), [rb2] "v"(rb2), [rb3] "v"(rb3)
-                    : "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168",
-                      "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177",
-                      "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186",
-                      "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195",
-                      "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204",
-                      "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213",
-                      "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222",
-                      "v223", "scc", "memory");
+#define FDL_DMA_LOOP_COMMON_OUT                                                           \
+    [cnt] "+s"(cnt), [m0s] "=&s"(m0s), [soa] "+s"(soa), [sob] "+s"(sob)
+#define FDL_DMA_LOOP_COMMON_IN                                                            \
+    [ma0] "s"(ma0), [ma1] "s"(ma1), [ma2] "s"(ma2), [ma3] "s"(ma3), [mb0] "s"(mb0),          \
+        [mb1] "s"(mb1), [mb2] "s"(mb2), [mb3] "s"(mb3), [bstep] "s"(bstep), [rsa] "s"(rsa),  \
+        [rsb] "s"(rsb), [va0] "v"(va0), [va1] "v"(va1), [va2] "v"(va2), [va3] "v"(va3),      \
+        [vb0] "v"(vb0), [vb1] "v"(vb1), [vb2] "v"(vb2), [vb3] "v"(vb3)
+#define FDL_DMA_LOOP_CLOBBERS                                                             \
+    "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170",  \
+        "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180",     \
+        "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190",     \
+        "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200",     \
+        "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210",     \
+        "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220",     \
+        "v221", "v222", "v223", "scc", "memory"
+                if constexpr (BM == 256) {
+                    // the chunk rotation is the same for the four A blocks
+                    const uint32_t ra0 = ra(0, 0), ra1 = ra(1, 0);
+                    const uint32_t rb0 = rbl, rb1 = rbl + 128, rb2 = rbl + 256, rb3 = rbl + 384;
+                    asm volatile(FDL_DMA256W4_LOOP
+                        : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c02] "+a"(acc[0][2]),
+                          [c03] "+a"(acc[0][3]), [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]),
+                          [c12] "+a"(acc[1][2]), [c13] "+a"(acc[1][3]), [c20] "+a"(acc[2][0]),
+                          [c21] "+a"(acc[2][1]), [c22] "+a"(acc[2][2]), [c23] "+a"(acc[2][3]),
+                          [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]), [c32] "+a"(acc[3][2]),
+                          [c33] "+a"(acc[3][3]), FDL_DMA_LOOP_COMMON_OUT
+                        : FDL_DMA_LOOP_COMMON_IN, [ra0] "v"(ra0), [ra1] "v"(ra1),
+                          [rb0] "v"(rb0), [rb1] "v"(rb1), [rb2] "v"(rb2), [rb3] "v"(rb3)
+                        : FDL_DMA_LOOP_CLOBBERS);
+                } else {
+                    // the two A blocks' chunks rotate differently: a base per (group, block)
+                    const uint32_t ra00 = ra(0, 0), ra01 = ra(0, 1), ra10 = ra(1, 0), ra11 = ra(1, 1),
+                                   ra20 = ra(2, 0), ra21 = ra(2, 1), ra30 = ra(3, 0), ra31 = ra(3, 1);
+                    const uint32_t rb0 = rbl, rb1 = rbl + 128;
+                    asm volatile(FDL_DMA128W4_LOOP
+                        : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c10] "+a"(acc[1][0]),
+                          [c11] "+a"(acc[1][1]), FDL_DMA_LOOP_COMMON_OUT
+                        : FDL_DMA_LOOP_COMMON_IN, [ra00] "v"(ra00), [ra01] "v"(ra01),
+                          [ra10] "v"(ra10), [ra11] "v"(ra11), [ra20] "v"(ra20), [ra21] "v"(ra21),
+                          [ra30] "v"(ra30), [ra31] "v"(ra31), [rb0] "v"(rb0), [rb1] "v"(rb1)
+                        : FDL_DMA_LOOP_CLOBBERS);
+                }
+#undef FDL_DMA_LOOP_COMMON_OUT
+#undef FDL_DMA_LOOP_COMMON_IN
+#undef FDL_DMA_LOOP_CLOBBERS
             }
         }
         // Group 0 of tile t (stage 0: t is 0 or a multiple of 3).
@@ -1922,10 +1949,11 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
     return hipGetLastError();
 }
 
-// Whether CfgDma256W4 runs this Dma256 problem: NN, K of at least 16
-// K-tiles, and each operand's extent (one batch) below 2 GiB, so the loop's
-// 32-bit buffer offsets (lane part plus K-tile part) cannot wrap.
-bool dma256w4_ok(const GemmParams& p, bool ta, bool tb) {
+// Whether a hand-scheduled four-wave loop (CfgDma256W4, CfgDma128W4) runs
+// this problem: NN, K of at least 256, and each operand's extent (one batch)
+// below 2 GiB, so the loop's 32-bit buffer offsets (lane part plus K-tile
+// part) cannot wrap.
+bool dma_w4_ok(const GemmParams& p, bool ta, bool tb) {
     constexpr int64_t kLimit = int64_t(1) << 31;
     const int64_t a_bytes = ((int64_t)(p.M - 1) * p.lda + p.K) * 4;
     const int64_t b_bytes = ((int64_t)(p.K - 1) * p.ldb + p.N) * 4;
@@ -2221,6 +2249,10 @@ using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
 // in the same order).
 using CfgDma256W4 = DmaCfg<256, 256, 16, 128, 128, 3, 1, 1, 1, 4, 1, 1>;
 using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
+// The same tile with three stages and the hand-scheduled loop of
+// dma_loops.inc (96 KB of LDS: one block per CU), for NN problems where the
+// eight-wave 128x128 tile runs one tile per CU.
+using CfgDma128W4 = DmaCfg<128, 128, 32, 64, 64, 3, 1, 1, 1, 4, 1, 1>;
 // 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU.  Two
 // sets of four 32x32 waves split each K-tile's k-groups, so one block per CU
 // still runs two waves per SIMD (1024^3: 24.3 vs 25.9 us with one set, and
@@ -2607,7 +2639,7 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 break;
             }
             case GemmKernel::Dma256:
-                err = dma256w4_ok(p, transA, transB)
+                err = dma_w4_ok(p, transA, transB)
                           ? launch_dma<CfgDma256W4>(p, transA, transB, nb, stream)
                           : launch_dma<CfgDma256>(p, transA, transB, nb, stream);
                 break;
@@ -2618,7 +2650,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 err = launch_dma_fit<CfgDma64S3, CfgDma64>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma128W8:
-                err = launch_dma<CfgDma128W8>(p, transA, transB, nb, stream);
+                err = dma_w4_ok(p, transA, transB)
+                          ? launch_dma<CfgDma128W4>(p, transA, transB, nb, stream)
+                          : launch_dma<CfgDma128W8>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma64U:
                 err = launch_dma_fit<CfgDma64US3, CfgDma64U>(p, transA, transB, nb, stream);

@@ -1,10 +1,10 @@
-"""GPU parity of the four-wave 256x256x16 tile and its hand-scheduled K loop
-(CfgDma256W4 in sgemm.hip, the loop in dma256_loop.inc), which runs the NN
-problems FDL_KERNEL_DMA256 takes with K >= 256.
+"""GPU parity of the four-wave tiles with hand-scheduled K loops (sgemm.hip's
+CfgDma256W4 and CfgDma128W4, the loops in dma_loops.inc), which run the NN
+problems FDL_KERNEL_DMA256 and FDL_KERNEL_DMA128W8 take with K >= 256.
 
 Each output adds the same products in the same order as the eight-wave
-kernel that runs the other layouts, so NN results must equal TN results (A
-stored transposed) bit for bit.  K values cover every way the asm loop hands
+kernels that run the other layouts, so NN results must equal TN results (A
+stored transposed) bit for bit.  K values cover every way the asm loops hand
 over to the compiled loop: whole groups of three steady K-tiles, then zero,
 one or two more steady tiles and the checked last tiles, with and without a
 partial last K-tile."""
@@ -16,9 +16,11 @@ from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, s
 
 pytestmark = pytest.mark.gpu
 
-DMA256 = capi.KERNEL_DMA256
-# K in K-tiles of 16: 16..21 K-tiles give (K-tiles - 2) % 3 = 2, 0, 1, 2, 0, 1;
-# 4100 and 1000 end in a partial K-tile; 255 stays below the loop's threshold.
+FAMS = [capi.KERNEL_DMA256, capi.KERNEL_DMA128W8]
+# K-tiles of 16 (256x256 tile): 16..21 K-tiles give (K-tiles - 2) % 3 = 2, 0,
+# 1, 2, 0, 1; K-tiles of 32 (128x128 tile): 8, 9 (partial), 9, 10 (partial),
+# 10, 11 (partial).  1000 and 4100 end in a partial K-tile; 252 stays below
+# the loops' threshold.
 KS = [256, 272, 288, 304, 320, 336, 1000, 4100, 252]
 
 
@@ -26,42 +28,46 @@ def _rng(*key):
     return np.random.default_rng(abs(hash(key)) & 0xFFFFFFFF)
 
 
+@pytest.mark.parametrize("fam", FAMS)
 @pytest.mark.parametrize("K", KS)
-def test_w4_matches_eight_wave_bitwise(device, K):
+def test_w4_matches_eight_wave_bitwise(device, fam, K):
     M, N = 520, 300
     g = _rng("w4", K)
     A, B = operands(g, 0, 0, M, N, K, 1)
     At = np.ascontiguousarray(np.swapaxes(A, 1, 2))
-    say(f"dma256 four-wave NN vs eight-wave TN, K={K}")
-    c_nn = gpu_sgemm(0, 0, A, B, M, N, K, kernel=DMA256)
-    c_tn = gpu_sgemm(1, 0, At, B, M, N, K, kernel=DMA256)
+    say(f"fam={fam} four-wave NN vs eight-wave TN, K={K}")
+    c_nn = gpu_sgemm(0, 0, A, B, M, N, K, kernel=fam)
+    c_tn = gpu_sgemm(1, 0, At, B, M, N, K, kernel=fam)
     assert np.array_equal(c_nn.view(np.uint32), c_tn.view(np.uint32))
     check_gemm(c_nn, 0, 0, A, B, M, N, K, fp32_oracle=False)
 
 
+@pytest.mark.parametrize("fam", FAMS)
 @pytest.mark.parametrize("epi", [capi.EPILOGUE_NONE, capi.EPILOGUE_BIAS, capi.EPILOGUE_BIAS_RELU,
                                  capi.EPILOGUE_RELU])
-def test_w4_epilogues_and_batch(device, epi):
+def test_w4_epilogues_and_batch(device, fam, epi):
     M, N, K, batch = 300, 520, 304, 3
     g = _rng("w4e", epi)
     A, B = operands(g, 0, 0, M, N, K, batch)
     bias = g.standard_normal(N).astype(np.float32)
-    say(f"dma256 four-wave epilogue {epi}, batch {batch}")
-    c = gpu_sgemm(0, 0, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, kernel=DMA256)
+    say(f"fam={fam} four-wave epilogue {epi}, batch {batch}")
+    c = gpu_sgemm(0, 0, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, kernel=fam)
     check_gemm(c, 0, 0, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, fp32_oracle=False)
 
 
-def test_w4_integer_inputs_exact(device):
+@pytest.mark.parametrize("fam", FAMS)
+def test_w4_integer_inputs_exact(device, fam):
     # Small integers: every partial sum is exact in fp32, so any order agrees.
     M, N, K = 512, 512, 1024
     A, B = operands(_rng("w4i"), 0, 0, M, N, K, 1, dist="int")
-    say("dma256 four-wave integer inputs")
-    c = gpu_sgemm(0, 0, A, B, M, N, K, kernel=DMA256)
+    say(f"fam={fam} four-wave integer inputs")
+    c = gpu_sgemm(0, 0, A, B, M, N, K, kernel=fam)
     exact = (A[0].astype(np.float64) @ B[0].astype(np.float64))
     assert np.array_equal(c[0].astype(np.float64), exact)
 
 
-def test_w4_padded_leading_dimensions(device):
+@pytest.mark.parametrize("fam", FAMS)
+def test_w4_padded_leading_dimensions(device, fam):
     M, N, K = 260, 520, 512
     g = _rng("w4p")
     A, B = operands(g, 0, 0, M, N, K, 1)
@@ -69,14 +75,15 @@ def test_w4_padded_leading_dimensions(device):
     Ap[:, :, :K] = A
     Bp = np.zeros((1, K, N + 12), np.float32)
     Bp[:, :, :N] = B
-    say("dma256 four-wave padded lda/ldb/ldc")
-    c = gpu_sgemm(0, 0, Ap, Bp, M, N, K, kernel=DMA256, lda=K + 36, ldb=N + 12, ldc=N + 8)
+    say(f"fam={fam} four-wave padded lda/ldb/ldc")
+    c = gpu_sgemm(0, 0, Ap, Bp, M, N, K, kernel=fam, lda=K + 36, ldb=N + 12, ldc=N + 8)
     check_gemm(c, 0, 0, A, B, M, N, K)
 
 
-def test_w4_operand_past_two_gib_falls_back(device):
+@pytest.mark.parametrize("fam", FAMS)
+def test_w4_operand_past_two_gib_falls_back(device, fam):
     """A spans more than 2 GiB (an lda of 2^23 + 64 floats over 65 rows): the
-    four-wave loop's 32-bit copy offsets are not used, the eight-wave kernel
+    four-wave loops' 32-bit copy offsets are not used, the eight-wave kernel
     runs, and the result is still right."""
     import torch
 
@@ -84,13 +91,13 @@ def test_w4_operand_past_two_gib_falls_back(device):
     lda = (1 << 23) + 64
     g = _rng("w4big")
     A, B = operands(g, 0, 0, M, N, K, 1)
-    say("dma256 with a 2.2 GB A (lda 2^23 + 64)")
+    say(f"fam={fam} with a 2.2 GB A (lda 2^23 + 64)")
     dA = torch.zeros((M, lda), dtype=torch.float32, device="cuda")
     dA[:, :K] = torch.from_numpy(A[0]).cuda()
     dB = dev(B)
     dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
     capi.sgemm_ex_select(0, 0, M, N, K, dA.data_ptr(), lda, M * lda, dB.data_ptr(), N, K * N,
-                         dC.data_ptr(), N, M * N, 1, None, None, 0, DMA256, stream())
+                         dC.data_ptr(), N, M * N, 1, None, None, 0, fam, stream())
     c = host(dC)[None]
     del dA
     check_gemm(c, 0, 0, A, B, M, N, K, fp32_oracle=False)
