@@ -106,8 +106,8 @@ int sgemm_impl(int transA, int transB, int64_t M, int64_t N, int64_t K, const fl
          kern == fdl::GemmKernel::Dma64S) &&
         !fdl::dma_supported(kern, p, ta, tb, batch)) {
         return fail(FDL_ERROR_NOT_SUPPORTED,
-                    "sgemm: the 16-byte direct-to-LDS kernels need K % 4 == 0 and "
-                    "16-byte-vectorisable operands");
+                    "sgemm: the 16-byte direct-to-LDS kernels need K % 4 == 0, "
+                    "16-byte-vectorisable operands and leading dimensions up to 2^22");
     }
     if ((kern == fdl::GemmKernel::Dma64U || kern == fdl::GemmKernel::Dma128W8U ||
          kern == fdl::GemmKernel::Dma96x32U) &&

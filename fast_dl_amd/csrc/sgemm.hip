@@ -553,6 +553,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_buffer(const float* base) 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, kBufferWord3);
 }
 
+// The same with 16 bytes per lane (lane i writes lds + 4 i floats).
+__device__ __forceinline__ void dma_buf_copy16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off,
+                                               float* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, byte_off, 0, 0, 0);
+}
+
 __device__ __forceinline__ void dma_buf_copy4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off,
                                               float* lds) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 4, byte_off, 0, 0, 0);
@@ -605,16 +611,14 @@ struct DmaOperand {
     // 4-byte copies each lane places its own element, so a copy may.
     static_assert(CW == 1 || KC || (kWave * CW) % MN == 0 || MN % (kWave * CW) == 0,
                   "mn-contiguous rows must tile the 64-lane copies");
-    // Global offset of each copy at k0 = 0.  With CW = 4 it is a 64-bit
-    // value per lane (goff).  With CW = 1 it is the wave's base (gb0, the row
-    // of its first copy; wave-uniform, so in scalar registers) plus a 32-bit
-    // lane part per copy (lo): the 2-4x more copies cost one VGPR each.  The
-    // lane part spans at most PER rows: callers keep ld * PER below 2^31.
-    static constexpr int P4 = CW == 4 ? PER : 1;
-    static constexpr int P1 = CW == 1 ? PER : 1;
-    int64_t goff[P4];
+    // Global offset of each copy at k0 = 0: the wave's base (gb0, the row of
+    // its first copy; wave-uniform, so in scalar registers) plus a 32-bit
+    // lane part per copy (lo), one VGPR per copy.  The copies are buffer
+    // loads from a descriptor at the wave's base, so no copy needs a 64-bit
+    // address.  The lane part spans the wave's copies' rows (at most 64):
+    // callers keep leading dimensions below kDmaMaxLd.
     int64_t gb0;
-    int lo[P1];
+    int lo[PER];
     int loff[PER];      // wave-uniform LDS offset (floats) of each copy within a stage
 
     // Position (in the tile) of copy unit `slot`: the operand row or k row
@@ -646,18 +650,10 @@ struct DmaOperand {
             const int ins = ins_of(wave, i);
             int r, c;
             place(ins * kWave + lane, r, c);
-            if constexpr (CW == 4) {
-                if (KC) {
-                    goff[i] = (int64_t)min(mn0 + r, mn_lim - 1) * ld + c;
-                } else {
-                    goff[i] = (int64_t)r * ld + min(mn0 + c, mn_lim - 4);
-                }
+            if (KC) {
+                lo[i] = (int)((int64_t)(min(mn0 + r, mn_lim - 1) - row0) * ld) + c;
             } else {
-                if (KC) {
-                    lo[i] = (int)((int64_t)(min(mn0 + r, mn_lim - 1) - row0) * ld) + c;
-                } else {
-                    lo[i] = (int)((int64_t)(r - row0) * ld) + min(mn0 + c, mn_lim - 1);
-                }
+                lo[i] = (int)((int64_t)(r - row0) * ld) + min(mn0 + c, mn_lim - CW);
             }
             loff[i] = ins * kWave * CW;
         }
@@ -698,16 +694,18 @@ struct DmaOperand {
         static_assert(0 <= I0 && I0 <= I1 && I1 <= PER, "a range of this tile's copies");
         if constexpr (I0 < I1) {
             const int64_t koff = KC ? (int64_t)k0 : (int64_t)k0 * ld;
-            if constexpr (CW == 4) {
+            // The tile's wave-uniform base in a buffer descriptor (scalar
+            // registers), each copy's lane part as a 32-bit offset from it.
+            // (4096^3 from global_load_lds with 64-bit addresses: 909.5 ->
+            // 905.8 us; 1024^3 20.8 -> 19.5 us; 1536^3 79.7 -> 72.9 us.)
+            const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
 #pragma unroll
-                for (int i = I0; i < I1; ++i) copy(base + goff[i] + koff, stage + loff[i]);
-            } else {
-                // The tile's wave-uniform base in a buffer descriptor (scalar
-                // registers), each copy's lane part as a 32-bit offset from it.
-                const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
-#pragma unroll
-                for (int i = I0; i < I1; ++i)
+            for (int i = I0; i < I1; ++i) {
+                if constexpr (CW == 4) {
+                    dma_buf_copy16(rsrc, (uint32_t)lo[i] * 4u, stage + loff[i]);
+                } else {
                     dma_buf_copy4(rsrc, (uint32_t)lo[i] * 4u, stage + loff[i]);
+                }
             }
         }
     }
@@ -720,7 +718,7 @@ struct DmaOperand {
         for (int i = 0; i < PER; ++i) {
             int r, c;
             place(ins_of(wave, i) * kWave + lane, r, c);
-            const int64_t g = CW == 4 ? goff[i] : gb0 + lo[i];
+            const int64_t g = gb0 + lo[i];
             int64_t off;
             if (KC) {
                 off = g - c + min(k0 + c, K - CW);
@@ -1027,10 +1025,11 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                 // scalar (tile 2 first); the host keeps every offset below 2^31.
                 const __amdgpu_buffer_rsrc_t rsa = dma_buffer(uniform(A));
                 const __amdgpu_buffer_rsrc_t rsb = dma_buffer(uniform(B));
-                const uint32_t va0 = (uint32_t)(opa.goff[0] * 4), va1 = (uint32_t)(opa.goff[1] * 4),
-                               va2 = (uint32_t)(opa.goff[2] * 4), va3 = (uint32_t)(opa.goff[3] * 4);
-                const uint32_t vb0 = (uint32_t)(opb.goff[0] * 4), vb1 = (uint32_t)(opb.goff[1] * 4),
-                               vb2 = (uint32_t)(opb.goff[2] * 4), vb3 = (uint32_t)(opb.goff[3] * 4);
+                auto full = [](int64_t gb, int lane_part) { return (uint32_t)((gb + lane_part) * 4); };
+                const uint32_t va0 = full(opa.gb0, opa.lo[0]), va1 = full(opa.gb0, opa.lo[1]),
+                               va2 = full(opa.gb0, opa.lo[2]), va3 = full(opa.gb0, opa.lo[3]);
+                const uint32_t vb0 = full(opb.gb0, opb.lo[0]), vb1 = full(opb.gb0, opb.lo[1]),
+                               vb2 = full(opb.gb0, opb.lo[2]), vb3 = full(opb.gb0, opb.lo[3]);
                 uint32_t soa = 2 * BK * 4;
                 uint32_t sob = __builtin_amdgcn_readfirstlane((uint32_t)(2 * BK * p.ldb * 4));
                 const uint32_t bstep = __builtin_amdgcn_readfirstlane((uint32_t)(BK * p.ldb * 4));
@@ -2342,6 +2341,9 @@ bool is_dma(GemmKernel k) {
 // Largest leading dimension of the 4-byte-copy kernels: a copy's 32-bit
 // lane offset spans up to 32 rows of 4-byte elements.
 constexpr int64_t kDma4MaxLd = int64_t(1) << 24;
+// Largest leading dimension of the 16-byte-copy kernels: a wave's copies span
+// up to 64 rows, so its 32-bit lane offsets stay below 2^31 bytes.
+constexpr int64_t kDmaMaxLd = int64_t(1) << 22;
 
 // Shape part of a direct-to-LDS kernel's contract (pointers not needed).
 bool dma_shape_ok(GemmKernel k, const GemmParams& p, bool transA, bool transB) {
@@ -2349,7 +2351,7 @@ bool dma_shape_ok(GemmKernel k, const GemmParams& p, bool transA, bool transB) {
     const int64_t a_contig = transA ? p.M : p.K;
     const int64_t b_contig = transB ? p.K : p.N;
     return p.K >= 4 && p.K % 4 == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
-           p.lda % 4 == 0 && p.ldb % 4 == 0;
+           p.lda % 4 == 0 && p.ldb % 4 == 0 && p.lda <= kDmaMaxLd && p.ldb <= kDmaMaxLd;
 }
 
 inline bool aligned4(const void* ptr) {

@@ -156,6 +156,8 @@ def test_dma_refuses_unsupported_problems(device):
 
     buf = torch.zeros(1 << 20, device="cuda")
     p = buf.data_ptr()
+    big = torch.zeros(4 * ((1 << 22) + 4) + 64, device="cuda")
+    pb = big.data_ptr()
     say("dma refusals")
     for fam, _ in DMAS16:
         # K not a multiple of 4
@@ -167,6 +169,10 @@ def test_dma_refuses_unsupported_problems(device):
         assert _raw_select(0, 0, 64, 64, 32, p, 33, p, 64, p, fam) == -2
         # N (B's contiguous extent) not a multiple of 4
         assert _raw_select(0, 0, 64, 66, 32, p, 32, p, 66, p, fam) == -2
+        # leading dimension past 2^22 (the copies' 32-bit lane offsets); the
+        # buffer covers what B's rows would span, so even a launch stays inside
+        assert _raw_select(0, 0, 64, 64, 4, pb, 4, pb, (1 << 22) + 4, p, fam) == -2
+        assert "2^22" in capi.last_error()
     for fam in (capi.KERNEL_DMA64U, capi.KERNEL_DMA128W8U, capi.KERNEL_DMA96X32U):
         # leading dimension past 2^24
         assert _raw_select(0, 0, 64, 64, 32, p, (1 << 24) + 1, p, 64, p, fam) == -2

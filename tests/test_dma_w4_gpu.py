@@ -82,22 +82,48 @@ def test_w4_padded_leading_dimensions(device, fam):
 
 @pytest.mark.parametrize("fam", FAMS)
 def test_w4_operand_past_two_gib_falls_back(device, fam):
-    """A spans more than 2 GiB (an lda of 2^23 + 64 floats over 65 rows): the
-    four-wave loops' 32-bit copy offsets are not used, the eight-wave kernel
-    runs, and the result is still right."""
+    """A spans more than 2 GiB (130 rows at lda = 2^22, the largest leading
+    dimension the direct-to-LDS kernels take): the four-wave loops' 32-bit
+    copy offsets are not used, the eight-wave kernel runs, and the result is
+    still right."""
     import torch
 
-    M, N, K = 65, 256, 512
-    lda = (1 << 23) + 64
+    M, N, K = 130, 256, 512
+    lda = 1 << 22
     g = _rng("w4big")
     A, B = operands(g, 0, 0, M, N, K, 1)
-    say(f"fam={fam} with a 2.2 GB A (lda 2^23 + 64)")
+    say(f"fam={fam} with a 2.2 GB A (lda 2^22)")
     dA = torch.zeros((M, lda), dtype=torch.float32, device="cuda")
     dA[:, :K] = torch.from_numpy(A[0]).cuda()
     dB = dev(B)
     dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
     capi.sgemm_ex_select(0, 0, M, N, K, dA.data_ptr(), lda, M * lda, dB.data_ptr(), N, K * N,
                          dC.data_ptr(), N, M * N, 1, None, None, 0, fam, stream())
+    c = host(dC)[None]
+    del dA
+    check_gemm(c, 0, 0, A, B, M, N, K, fp32_oracle=False)
+
+
+def test_leading_dimension_past_dma_limit(device):
+    """lda above 2^22 floats: forcing a direct-to-LDS kernel is refused
+    (FDL_ERROR_NOT_SUPPORTED) and the automatic choice takes another kernel."""
+    import torch
+
+    M, N, K = 8 * 64, 512, 256
+    lda = (1 << 22) + 4
+    g = _rng("ldbig")
+    A, B = operands(g, 0, 0, M, N, K, 1)
+    say("lda 2^22 + 4: forced dma256 refused, auto correct")
+    dA = torch.zeros((M, lda), dtype=torch.float32, device="cuda")
+    dA[:, :K] = torch.from_numpy(A[0]).cuda()
+    dB = dev(B)
+    dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    args = (0, 0, M, N, K, dA.data_ptr(), lda, M * lda, dB.data_ptr(), N, K * N,
+            dC.data_ptr(), N, M * N, 1, None, None, 0)
+    with pytest.raises(capi.FdlError) as err:
+        capi.sgemm_ex_select(*args, capi.KERNEL_DMA256, stream())
+    assert "2^22" in str(err.value)
+    capi.sgemm_ex_select(*args, capi.KERNEL_AUTO, stream())
     c = host(dC)[None]
     del dA
     check_gemm(c, 0, 0, A, B, M, N, K, fp32_oracle=False)
