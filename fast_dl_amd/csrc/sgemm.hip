@@ -549,6 +549,16 @@ __device__ __forceinline__ void dma_copy4(const float* g, float* lds) {
 // value for gfx9-family targets (gfx950 included).
 constexpr int kBufferWord3 = 0x00020000;
 
+// A pointer the caller knows to be the same on every lane, in scalar
+// registers: without this the compiler may treat a descriptor built from it
+// as divergent and wrap each buffer load in a loop over the lanes' values.
+__device__ __forceinline__ const float* wave_uniform(const float* q) {
+    const uint64_t v = (uint64_t)q;
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const float*)(lo | (hi << 32));
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_buffer(const float* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, kBufferWord3);
 }
@@ -698,7 +708,7 @@ struct DmaOperand {
             // registers), each copy's lane part as a 32-bit offset from it.
             // (4096^3 from global_load_lds with 64-bit addresses: 909.5 ->
             // 905.8 us; 1024^3 20.8 -> 19.5 us; 1536^3 79.7 -> 72.9 us.)
-            const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(base + (gb0 + koff));
+            const __amdgpu_buffer_rsrc_t rsrc = dma_buffer(wave_uniform(base + (gb0 + koff)));
 #pragma unroll
             for (int i = I0; i < I1; ++i) {
                 if constexpr (CW == 4) {
@@ -1014,17 +1024,11 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
             int cnt = (has_tail ? ktiles - 3 : ktiles - 2) / 3;
             if (cnt > 0) {
                 t = 3 * cnt;
-                auto uniform = [](const float* q) {
-                    const uint64_t v = (uint64_t)q;
-                    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-                    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-                    return (const float*)(lo | (hi << 32));
-                };
                 // Copies: each operand's base in a buffer descriptor, the lane
                 // offsets of the wave's four copies, the K-tile's offset in a
                 // scalar (tile 2 first); the host keeps every offset below 2^31.
-                const __amdgpu_buffer_rsrc_t rsa = dma_buffer(uniform(A));
-                const __amdgpu_buffer_rsrc_t rsb = dma_buffer(uniform(B));
+                const __amdgpu_buffer_rsrc_t rsa = dma_buffer(wave_uniform(A));
+                const __amdgpu_buffer_rsrc_t rsb = dma_buffer(wave_uniform(B));
                 auto full = [](int64_t gb, int lane_part) { return (uint32_t)((gb + lane_part) * 4); };
                 const uint32_t va0 = full(opa.gb0, opa.lo[0]), va1 = full(opa.gb0, opa.lo[1]),
                                va2 = full(opa.gb0, opa.lo[2]), va3 = full(opa.gb0, opa.lo[3]);
