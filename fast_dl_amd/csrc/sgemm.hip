@@ -2300,10 +2300,14 @@ struct TileModel {
     float eff[9];
 };
 
+// The direct-to-LDS rows were fitted to back-to-back times of 26 NN, TN and
+// NT problems from 1024^3 to 6144x6144x2048 and K from 64 to 4096 (the
+// model's pick within 2.4% of the fastest direct-to-LDS tile on 23 of them,
+// within 9% on the rest).
 constexpr TileModel kTileModels[] = {
-    {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f, 0.86f}},
+    {GemmKernel::Dma256, 256, 256, 1, 8, {0, 0.50f, 0.84f, 0.84f, 0.84f, 0.84f, 0.84f, 0.84f, 0.84f}},
     {GemmKernel::Dma128, 128, 128, 2, 4, {0, 0.75f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f, 0.83f}},
-    {GemmKernel::Dma64, 64, 64, 2, 8, {0, 0.57f, 0.57f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f, 0.69f}},
+    {GemmKernel::Dma64, 64, 64, 2, 8, {0, 0.57f, 0.57f, 0.57f, 0.90f, 0.90f, 0.90f, 0.90f, 0.90f}},
     {GemmKernel::Dma128W8, 128, 128, 1, 8, {0, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f, 0.78f}},
     {GemmKernel::Dma64U, 64, 64, 2, 8, {0, 0.553f, 0.553f, 0.67f, 0.67f, 0.67f, 0.67f, 0.67f, 0.67f}},
     {GemmKernel::Dma128W8U, 128, 128, 1, 8, {0, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f, 0.757f}},
@@ -2316,16 +2320,29 @@ constexpr TileModel kTileModels[] = {
     {GemmKernel::Tiled64, 64, 64, 8, 4, {0, 0.30f, 0.45f, 0.52f, 0.60f, 0.63f, 0.65f, 0.67f, 0.68f}},
 };
 
-double predicted_time(const TileModel& t, int M, int N, int64_t batch) {
+// Where the four-wave hand-scheduled form runs (NN, dma_w4_ok), Dma256 and
+// Dma128W8 are faster than their rows above say (4096^3: 0.95; 2048^3 and
+// 6144x6144x2048: 0.93).
+constexpr float kW4Eff256 = 0.95f;
+constexpr float kW4Eff128 = 0.93f;
+
+// Each round of co-resident blocks also pays a fixed cost (its first
+// copies' round trip and its stores), about 1 us, here in the same unit as
+// the work: FMAs at one CU's fp32 MFMA rate (128 per clock at 2.4 GHz).  It
+// matters only for short K (4096x4096x192: the 256x256 tile at 56 us against
+// 68 us for the 64x64 tile's eight rounds).
+constexpr double kRoundCost = 3.07e5;
+
+double predicted_time(const TileModel& t, int M, int N, int K, int64_t batch) {
     constexpr int64_t kCUs = 256;
     const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
     const int64_t per_cu = (tiles + kCUs - 1) / kCUs;
-    const double work = (double)t.bm * t.bn;
+    const double work = (double)t.bm * t.bn * K;
     const int64_t full = per_cu / t.slots;
     const int64_t rest = per_cu % t.slots;
     auto round_cost = [&](int64_t blocks) {
         const int w = (int)std::min<int64_t>(8, std::max<int64_t>(1, blocks * t.waves / 4));
-        return (double)blocks * work / t.eff[w];
+        return (double)blocks * work / t.eff[w] + kRoundCost;
     };
     double time = (double)full * round_cost(t.slots);
     if (rest) time += round_cost(rest);
@@ -2431,7 +2448,14 @@ GemmKernel choose_kernel(const GemmParams& p, bool transA, bool transB,
         for (const TileModel& t : kTileModels) {
             if (is_dma(t.kernel) != (pass == 0)) continue;
             if (is_dma(t.kernel) && !dma_shape_ok(t.kernel, p, transA, transB)) continue;
-            const double tm = predicted_time(t, p.M, p.N, batch);
+            TileModel tw = t;
+            if ((t.kernel == GemmKernel::Dma256 || t.kernel == GemmKernel::Dma128W8) &&
+                dma_w4_ok(p, transA, transB)) {
+                for (int w = 1; w <= 8; ++w)
+                    tw.eff[w] = t.kernel == GemmKernel::Dma256 ? kW4Eff256 : kW4Eff128;
+                tw.eff[1] = t.kernel == GemmKernel::Dma256 ? t.eff[1] : kW4Eff128;
+            }
+            const double tm = predicted_time(tw, p.M, p.N, p.K, batch);
             if (first || tm < best_time * 0.99) {  // ties keep the earlier (larger) tile
                 best = t.kernel;
                 best_time = tm;
