@@ -219,7 +219,10 @@ struct TileLoader {
 // that read aux or update a parameter.
 constexpr int kBufferWord3Store = 0x00020000;  // raw-buffer descriptor word 3 (gfx9 family)
 
-template <int FM, int FN>
+// STREAM = 1: the fast path's stores are non-temporal (buffer store `nt`), for
+// tiles that only large outputs use (2048^3: 119.8 -> 118.6 us; 4096^3 and
+// 8192^3 within 0.3%).
+template <int FM, int FN, int STREAM = 0>
 __device__ __forceinline__ void store_wave_tile(floatx16 (&acc)[FM][FN], const GemmParams& p,
                                                 int64_t bz, int mw, int nw, int half,
                                                 int l32, const float* bias_pre = nullptr) {
@@ -258,7 +261,7 @@ __device__ __forceinline__ void store_wave_tile(floatx16 (&acc)[FM][FN], const G
                             const float v = op(acc[mi][ni][r], bj[ni]);
                             __builtin_amdgcn_raw_buffer_store_b32(
                                 __builtin_bit_cast(uint32_t, v), rsrc, (int)lane_off,
-                                (row * ldc + ni * 32) * 4, 0);
+                                (row * ldc + ni * 32) * 4, STREAM ? 2 : 0);  // 2: nt
                         }
             };
             if (has_bias && relu) {
@@ -1302,7 +1305,9 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                         acc[mi][ni][r] += src[((mi * FN + ni) * 16 + r) * kWave];
         }
     }
-    store_wave_tile<FM, FN>(acc, p, bz, m0 + wm0, n0 + wn0, half, l32, bias_pre);
+    // The 128- and 256-row tiles run only where C is at least about 8 MiB.
+    store_wave_tile<FM, FN, (BM >= 128 && BN >= 128) ? 1 : 0>(acc, p, bz, m0 + wm0, n0 + wn0,
+                                                               half, l32, bias_pre);
 }
 
 // ---------------------------------------------------------------------------
