@@ -4,8 +4,9 @@ four-wave direct-to-LDS tiles of sgemm.hip, one inline-asm statement each.
     python fast_dl_amd/csrc/gen_dma_loops.py fast_dl_amd/csrc/dma_loops.inc
 
 Each loop is the compiler-scheduled XPIPE loop of sgemm_dma_kernel with three
-LDS stages, NN layout, written out instruction by instruction so that every
-MFMA, fragment read, copy and wait sits where it is placed here:
+LDS stages, for one operand layout (NN, NT, TN or TT), written out
+instruction by instruction so that every MFMA, fragment read, copy and wait
+sits where it is placed here:
 
   * four waves, one per SIMD, each owning a WM x WN block of the tile as
     FM x FN accumulators of 32x32 (AGPRs, operands %[c<mi><ni>]);
@@ -25,9 +26,17 @@ MFMA, fragment read, copy and wait sits where it is placed here:
     and every LDS offset is an immediate.
 
 Fragments live in fixed registers from v160 (clobbered by the statement):
-slot s, A block mi: 4 registers (one ds_read_b128: the four k values of a
-lane's row in the group); B block ni: 4 registers (two ds_read2st64_b32: k
-rows BN floats apart).  Measured on MI355X at 4096^3 (256x256 tile): 945 us
+slot s, A block mi and B block ni: 4 registers each, the four k values of the
+lane's row or column in the group.  A k-contiguous operand (A in NN/NT, B in
+NT/TT) is read with one ds_read_b128 from its rotated 16-byte k-chunk; an
+mn-contiguous one (A in TN/TT, B in NN/TN) with two ds_read2st64_b32 of k rows
+MN floats apart.
+
+For each loop the file defines <NAME>_TEXT (the statement), <NAME>_ACC (its
+accumulator operands, acc[mi][ni]) and <NAME>_READS (its fragment read
+bases: rka[g][mi] / rkb[g][ni] for a k-contiguous operand, the block's base
+for group g; rma[mi] / rmb[ni] for an mn-contiguous one, the lane's column at
+k row 4 * half).  Measured on MI355X at 4096^3 (256x256 tile): 945 us
 for the compiler-scheduled eight-wave tile, 930 us for this loop with
 global_load_lds copies, 911-920 us with buffer copies.
 """
@@ -45,6 +54,8 @@ class Loop:
     wn: int
     read_every: int       # MFMAs between two fragment reads
     copy_slots: tuple     # MFMAs of a group after which its copies go
+    a_kc: bool = True     # A k-contiguous (not transposed)
+    b_kc: bool = False    # B k-contiguous (transposed)
     nt: int = 256
     stages: int = 3
 
@@ -76,12 +87,13 @@ class Loop:
     def per_b(self):
         return self.bk * self.bn // 4 // self.nt
 
-    def a_base_per_mi(self):
-        """Whether a lane's rotated k-chunk differs between its A blocks (the
-        rotation of a k-contiguous row r is kc_swz(r); blocks are 32 rows apart)."""
+    def base_per_block(self, blocks):
+        """Whether a lane's rotated k-chunk differs between its blocks of a
+        k-contiguous operand (the rotation of row r is kc_swz(r); blocks are
+        32 rows apart)."""
         cpr = self.bk // 4
         swz = {4: lambda r: (r >> 2) & 3, 8: lambda r: (r ^ (r >> 3)) & 7, 16: lambda r: r & 15}[cpr]
-        return any(swz(r) != swz(r + 32 * mi) for r in range(64) for mi in range(self.fm))
+        return any(swz(r) != swz(r + 32 * b) for r in range(64) for b in range(blocks))
 
 
 def emit(L: Loop) -> list:
@@ -89,7 +101,7 @@ def emit(L: Loop) -> list:
     slot_regs = 4 * (fm + fn)
     assert 160 + 2 * slot_regs <= 256
     per_tile = L.per_a + L.per_b
-    per_mi = L.a_base_per_mi()
+    operands = {}   # read-base operand name -> C++ expression
 
     def areg(s, mi):
         return 160 + slot_regs * s + 4 * mi
@@ -97,24 +109,45 @@ def emit(L: Loop) -> list:
     def breg(s, ni):
         return 160 + slot_regs * s + 4 * fm + 4 * ni
 
-    def reads(slot, g, stage):
+    def kc_reads(x, reg, blocks, g, stage, stage_bytes):
+        # k-contiguous rows of BK floats, 16-byte chunks rotated per row
         out = []
-        for mi in range(fm):
-            r = areg(slot, mi)
-            if per_mi:   # %[ra<g><mi>]: the lane's row start plus its rotated k-chunk
-                out.append(f"ds_read_b128 v[{r}:{r + 3}], %[ra{g}{mi}] offset:{stage * L.stage_a}")
-            else:        # %[ra<g>]: the same for block 0; blocks are 32 rows apart
-                out.append(f"ds_read_b128 v[{r}:{r + 3}], %[ra{g}] "
-                           f"offset:{stage * L.stage_a + mi * 32 * L.bk * 4}")
-        row_units = L.bn * 4 // 256   # one k row of B, in ds_read2st64's 256-byte units
-        for ni in range(fn):
-            r = breg(slot, ni)
+        per_block = L.base_per_block(blocks)
+        for b in range(blocks):
+            r = reg(b)
+            if per_block:   # the lane's row start plus its rotated k-chunk, per block
+                name, expr, off = f"r{x}{g}{b}", f"rk{x}[{g}][{b}]", stage * stage_bytes
+            else:           # block 0's; the blocks are 32 rows apart
+                name, expr, off = f"r{x}{g}", f"rk{x}[{g}][0]", stage * stage_bytes + b * 32 * L.bk * 4
+            operands[name] = expr
+            assert off < 65536
+            out.append(f"ds_read_b128 v[{r}:{r + 3}], %[{name}] offset:{off}")
+        return out
+
+    def mn_reads(x, reg, blocks, mn, g, stage, stage_bytes):
+        # k rows of MN floats; the lane's column at k row 4 * half
+        out = []
+        row_units = mn * 4 // 256   # one k row, in ds_read2st64's 256-byte units
+        for b in range(blocks):
+            r = reg(b)
+            name = f"r{x}m{b}"
+            operands[name] = f"rm{x}[{b}]"
             for p in range(2):
-                # %[rb<ni>]: the lane's column and k half
-                o0 = stage * L.stage_b // 256 + (8 * g + 2 * p) * row_units
+                o0 = stage * stage_bytes // 256 + (8 * g + 2 * p) * row_units
                 assert o0 + row_units <= 255
-                out.append(f"ds_read2st64_b32 v[{r + 2 * p}:{r + 2 * p + 1}], %[rb{ni}] "
+                out.append(f"ds_read2st64_b32 v[{r + 2 * p}:{r + 2 * p + 1}], %[{name}] "
                            f"offset0:{o0} offset1:{o0 + row_units}")
+        return out
+
+    def reads(slot, g, stage):
+        if L.a_kc:
+            out = kc_reads("a", lambda b: areg(slot, b), fm, g, stage, L.stage_a)
+        else:
+            out = mn_reads("a", lambda b: areg(slot, b), fm, L.bm, g, stage, L.stage_a)
+        if L.b_kc:
+            out += kc_reads("b", lambda b: breg(slot, b), fn, g, stage, L.stage_b)
+        else:
+            out += mn_reads("b", lambda b: breg(slot, b), fn, L.bn, g, stage, L.stage_b)
         return out
 
     def chunk_lo(g):
@@ -127,14 +160,16 @@ def emit(L: Loop) -> list:
                 "s_nop 0",   # M0 written by SALU, then read by an LDS DMA: one wait state
                 f"buffer_load_dwordx4 %[v{op}{j}], %[rs{op}], %[so{op}] offen lds"]
 
-    def advance(op):
-        return f"s_add_u32 %[so{op}], %[so{op}], {L.bk * 4 if op == 'a' else '%[bstep]'}"
+    def advance(op):   # %[astep], %[bstep]: one K-tile of the operand, in bytes
+        return f"s_add_u32 %[so{op}], %[so{op}], %[{op}step]"
 
     def group(slot, rd, cps, advances):
         out = []
         rd = list(rd)
         n = 4 * fm * fn
-        slots = [1 + L.read_every * i for i in range(len(rd))]
+        # a read every read_every MFMAs, closer where the layout has more reads
+        every = min(L.read_every, (n - 2) // max(1, len(rd) - 1))
+        slots = [1 + every * i for i in range(len(rd))]
         assert slots[-1] < n
         last_copy = max(L.copy_slots[:len(cps)]) if cps else -1
         for j in range(n):
@@ -187,20 +222,27 @@ def emit(L: Loop) -> list:
               "s_waitcnt lgkmcnt(0)",  # no read may land after the statement
               "s_nop 7", "s_nop 7", "s_nop 7",  # last MFMAs retire before the compiler reads AGPRs
               "s_mov_b32 m0, %[m0s]"]
-    out = [f"#define {L.macro} \\"]
+    out = [f"#define {L.macro}_TEXT \\"]
     out += [f'    "{line}\\n\\t" \\' for line in lines]
     out.append('    ""')
+    acc = [f'[c{mi}{ni}] "+a"(acc[{mi}][{ni}])' for mi in range(fm) for ni in range(fn)]
+    out.append(f"#define {L.macro}_ACC " + ", ".join(acc))
+    rd = [f'[{k}] "v"({v})' for k, v in operands.items()]
+    out.append(f"#define {L.macro}_READS " + ", ".join(rd))
     return out
 
 
-LOOPS = [
+LAYOUTS = {"NN": (True, False), "NT": (True, True), "TN": (False, False), "TT": (False, True)}
+LOOPS = []
+for lay, (a_kc, b_kc) in LAYOUTS.items():
     # 256x256x16, waves of 128x128 (CfgDma256W4): a read every 5 MFMAs from
     # the second, a group's four copies after its first four MFMAs.
-    Loop("FDL_DMA256W4_LOOP", 256, 256, 16, 128, 128, read_every=5, copy_slots=(1, 2, 3, 4)),
+    LOOPS.append(Loop(f"FDL_DMA256W4_{lay}", 256, 256, 16, 128, 128, read_every=5,
+                      copy_slots=(1, 2, 3, 4), a_kc=a_kc, b_kc=b_kc))
     # 128x128x32, waves of 64x64 (CfgDma128W4): four groups of 16 MFMAs, a
     # read every 2 MFMAs, a group's two copies after its first two MFMAs.
-    Loop("FDL_DMA128W4_LOOP", 128, 128, 32, 64, 64, read_every=2, copy_slots=(1, 2)),
-]
+    LOOPS.append(Loop(f"FDL_DMA128W4_{lay}", 128, 128, 32, 64, 64, read_every=2,
+                      copy_slots=(1, 2), a_kc=a_kc, b_kc=b_kc))
 
 
 def main(path):

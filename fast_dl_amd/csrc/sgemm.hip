@@ -518,7 +518,7 @@ sgemm_tiled_kernel(GemmParams p, int tiles_m, int tiles_n) {
 // CW is the copy width in floats per lane (4: 16-byte copies, which need
 // 16-byte-aligned operand rows and K % 4 == 0; 1: 4-byte copies, any shape).
 // ASM = 1: the steady-state K loop is a hand-scheduled one of dma_loops.inc
-// (CfgDma256W4 and CfgDma128W4 on NN problems; see its generator).
+// (CfgDma256W4 and CfgDma128W4, every layout; see its generator).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, int XPIPE_ = 0,
           int ILV_ = 0, int KS_ = 1, int CW_ = 4, int WPE_ = 1, int ASM_ = 0>
 struct DmaCfg {
@@ -1013,11 +1013,10 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         asm volatile("" ::: "memory");
         int t = 0;  // the next K-tile the C++ loops below run
         if constexpr (Cfg::ASM != 0) {
-            static_assert(!TA && !TB && S == 3 && KS == 1 && Cfg::CW == 4 && NT == 256 &&
+            static_assert(S == 3 && KS == 1 && Cfg::CW == 4 && NT == 256 &&
                               ((BM == 256 && BN == 256 && BK == 16 && FM == 4 && FN == 4) ||
                                (BM == 128 && BN == 128 && BK == 32 && FM == 2 && FN == 2)),
-                          "the hand-scheduled loops are written for CfgDma256W4 and CfgDma128W4 "
-                          "on NN problems");
+                          "the hand-scheduled loops are written for CfgDma256W4 and CfgDma128W4");
             static_assert(OpA::PER == 4 && OpB::PER == 4, "four copies of each operand per wave");
             // Whole groups of three steady K-tiles (tile t+2 full and inside
             // K) run in the asm loop; it starts where this code stands (tiles
@@ -1037,9 +1036,14 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                                va2 = full(opa.gb0, opa.lo[2]), va3 = full(opa.gb0, opa.lo[3]);
                 const uint32_t vb0 = full(opb.gb0, opb.lo[0]), vb1 = full(opb.gb0, opb.lo[1]),
                                vb2 = full(opb.gb0, opb.lo[2]), vb3 = full(opb.gb0, opb.lo[3]);
-                uint32_t soa = 2 * BK * 4;
-                uint32_t sob = __builtin_amdgcn_readfirstlane((uint32_t)(2 * BK * p.ldb * 4));
-                const uint32_t bstep = __builtin_amdgcn_readfirstlane((uint32_t)(BK * p.ldb * 4));
+                // one K-tile of each operand in bytes: BK floats along a
+                // k-contiguous row, BK rows of an mn-contiguous operand
+                const uint32_t astep = __builtin_amdgcn_readfirstlane(
+                    (uint32_t)(TA ? BK * p.lda * 4 : BK * 4));
+                const uint32_t bstep = __builtin_amdgcn_readfirstlane(
+                    (uint32_t)(TB ? BK * 4 : BK * p.ldb * 4));
+                uint32_t soa = 2 * astep;
+                uint32_t sob = 2 * bstep;
                 // LDS byte addresses: each copy's wave base (M0, before the
                 // stage offset) and the lanes' fragment read bases.
                 const uint32_t lds_a = (uint32_t)(uintptr_t)As;
@@ -1052,59 +1056,71 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                 const uint32_t mb1 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[1] * 4);
                 const uint32_t mb2 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[2] * 4);
                 const uint32_t mb3 = __builtin_amdgcn_readfirstlane(lds_b + opb.loff[3] * 4);
-                // As OpA::read: row r's 16-byte k-chunk (2g + half) rotated by
-                // kc_swz(r); as OpB::read: column, k row 4 * half.
-                auto ra = [&](int g, int mi) {
-                    const int r = wm0 + mi * 32 + l32;
-                    return lds_a + r * BK * 4 + 16 * ((2 * g + half) ^ kc_swz<OpA::CPR>(r));
-                };
-                const uint32_t rbl = lds_b + (4 * half * BN + wn0 + l32) * 4;
-                int m0s;
-#define FDL_DMA_LOOP_COMMON_OUT                                                           \
-    [cnt] "+s"(cnt), [m0s] "=&s"(m0s), [soa] "+s"(soa), [sob] "+s"(sob)
-#define FDL_DMA_LOOP_COMMON_IN                                                            \
-    [ma0] "s"(ma0), [ma1] "s"(ma1), [ma2] "s"(ma2), [ma3] "s"(ma3), [mb0] "s"(mb0),          \
-        [mb1] "s"(mb1), [mb2] "s"(mb2), [mb3] "s"(mb3), [bstep] "s"(bstep), [rsa] "s"(rsa),  \
-        [rsb] "s"(rsb), [va0] "v"(va0), [va1] "v"(va1), [va2] "v"(va2), [va3] "v"(va3),      \
-        [vb0] "v"(vb0), [vb1] "v"(vb1), [vb2] "v"(vb2), [vb3] "v"(vb3)
-#define FDL_DMA_LOOP_CLOBBERS                                                             \
-    "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170",  \
-        "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180",     \
-        "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190",     \
-        "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200",     \
-        "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210",     \
-        "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220",     \
-        "v221", "v222", "v223", "scc", "memory"
-                if constexpr (BM == 256) {
-                    // the chunk rotation is the same for the four A blocks
-                    const uint32_t ra0 = ra(0, 0), ra1 = ra(1, 0);
-                    const uint32_t rb0 = rbl, rb1 = rbl + 128, rb2 = rbl + 256, rb3 = rbl + 384;
-                    asm volatile(FDL_DMA256W4_LOOP
-                        : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c02] "+a"(acc[0][2]),
-                          [c03] "+a"(acc[0][3]), [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]),
-                          [c12] "+a"(acc[1][2]), [c13] "+a"(acc[1][3]), [c20] "+a"(acc[2][0]),
-                          [c21] "+a"(acc[2][1]), [c22] "+a"(acc[2][2]), [c23] "+a"(acc[2][3]),
-                          [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]), [c32] "+a"(acc[3][2]),
-                          [c33] "+a"(acc[3][3]), FDL_DMA_LOOP_COMMON_OUT
-                        : FDL_DMA_LOOP_COMMON_IN, [ra0] "v"(ra0), [ra1] "v"(ra1),
-                          [rb0] "v"(rb0), [rb1] "v"(rb1), [rb2] "v"(rb2), [rb3] "v"(rb3)
-                        : FDL_DMA_LOOP_CLOBBERS);
-                } else {
-                    // the two A blocks' chunks rotate differently: a base per (group, block)
-                    const uint32_t ra00 = ra(0, 0), ra01 = ra(0, 1), ra10 = ra(1, 0), ra11 = ra(1, 1),
-                                   ra20 = ra(2, 0), ra21 = ra(2, 1), ra30 = ra(3, 0), ra31 = ra(3, 1);
-                    const uint32_t rb0 = rbl, rb1 = rbl + 128;
-                    asm volatile(FDL_DMA128W4_LOOP
-                        : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c10] "+a"(acc[1][0]),
-                          [c11] "+a"(acc[1][1]), FDL_DMA_LOOP_COMMON_OUT
-                        : FDL_DMA_LOOP_COMMON_IN, [ra00] "v"(ra00), [ra01] "v"(ra01),
-                          [ra10] "v"(ra10), [ra11] "v"(ra11), [ra20] "v"(ra20), [ra21] "v"(ra21),
-                          [ra30] "v"(ra30), [ra31] "v"(ra31), [rb0] "v"(rb0), [rb1] "v"(rb1)
-                        : FDL_DMA_LOOP_CLOBBERS);
+                // Fragment read bases, as DmaOperand::read.  A k-contiguous
+                // operand: row r's 16-byte k-chunk (2g + half) rotated by
+                // kc_swz(r), per k-group and block (rka, rkb).  An
+                // mn-contiguous one: the lane's column at k row 4 * half, per
+                // block (rma, rmb).  Each loop reads the ones its layout has.
+                uint32_t rka[NGK][FM], rkb[NGK][FN], rma[FM], rmb[FN];
+#pragma unroll
+                for (int g = 0; g < NGK; ++g) {
+#pragma unroll
+                    for (int mi = 0; mi < FM; ++mi) {
+                        const int r = wm0 + mi * 32 + l32;
+                        rka[g][mi] = lds_a + r * BK * 4 + 16 * ((2 * g + half) ^ kc_swz<OpA::CPR>(r));
+                    }
+#pragma unroll
+                    for (int ni = 0; ni < FN; ++ni) {
+                        const int r = wn0 + ni * 32 + l32;
+                        rkb[g][ni] = lds_b + r * BK * 4 + 16 * ((2 * g + half) ^ kc_swz<OpB::CPR>(r));
+                    }
                 }
-#undef FDL_DMA_LOOP_COMMON_OUT
-#undef FDL_DMA_LOOP_COMMON_IN
-#undef FDL_DMA_LOOP_CLOBBERS
+#pragma unroll
+                for (int mi = 0; mi < FM; ++mi) rma[mi] = lds_a + (4 * half * BM + wm0 + mi * 32 + l32) * 4;
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni) rmb[ni] = lds_b + (4 * half * BN + wn0 + ni * 32 + l32) * 4;
+                int m0s;
+#define FDL_W4_LOOP(NAME)                                                                 \
+    asm volatile(NAME##_TEXT                                                              \
+                 : NAME##_ACC, [cnt] "+s"(cnt), [m0s] "=&s"(m0s), [soa] "+s"(soa),       \
+                   [sob] "+s"(sob)                                                        \
+                 : [ma0] "s"(ma0), [ma1] "s"(ma1), [ma2] "s"(ma2), [ma3] "s"(ma3),        \
+                   [mb0] "s"(mb0), [mb1] "s"(mb1), [mb2] "s"(mb2), [mb3] "s"(mb3),        \
+                   [astep] "s"(astep), [bstep] "s"(bstep), [rsa] "s"(rsa), [rsb] "s"(rsb), \
+                   [va0] "v"(va0), [va1] "v"(va1), [va2] "v"(va2), [va3] "v"(va3),        \
+                   [vb0] "v"(vb0), [vb1] "v"(vb1), [vb2] "v"(vb2), [vb3] "v"(vb3),        \
+                   NAME##_READS                                                           \
+                 : "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167",        \
+                   "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175",        \
+                   "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183",        \
+                   "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191",        \
+                   "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199",        \
+                   "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207",        \
+                   "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215",        \
+                   "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "scc", \
+                   "memory")
+                if constexpr (BM == 256) {
+                    if constexpr (!TA && !TB) {
+                        FDL_W4_LOOP(FDL_DMA256W4_NN);
+                    } else if constexpr (!TA) {
+                        FDL_W4_LOOP(FDL_DMA256W4_NT);
+                    } else if constexpr (!TB) {
+                        FDL_W4_LOOP(FDL_DMA256W4_TN);
+                    } else {
+                        FDL_W4_LOOP(FDL_DMA256W4_TT);
+                    }
+                } else {
+                    if constexpr (!TA && !TB) {
+                        FDL_W4_LOOP(FDL_DMA128W4_NN);
+                    } else if constexpr (!TA) {
+                        FDL_W4_LOOP(FDL_DMA128W4_NT);
+                    } else if constexpr (!TB) {
+                        FDL_W4_LOOP(FDL_DMA128W4_TN);
+                    } else {
+                        FDL_W4_LOOP(FDL_DMA128W4_TT);
+                    }
+                }
+#undef FDL_W4_LOOP
             }
         }
         // Group 0 of tile t (stage 0: t is 0 or a multiple of 3).
@@ -1937,11 +1953,7 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
     const int flat = nbatch > 1 && tiles <= kFlatBatchMaxTiles;
     const dim3 grid = flat ? dim3(tiles * nbatch) : dim3(tiles, nbatch);
     const dim3 block(Cfg::NT);
-    if constexpr (Cfg::ASM != 0) {  // the hand-scheduled loop exists for NN only
-        if (ta || tb) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n, flat);
-    } else if (!ta && !tb) {
+    if (!ta && !tb) {
         hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
                            tiles_m, tiles_n, flat);
     } else if (!ta) {
@@ -1958,14 +1970,16 @@ hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStre
 }
 
 // Whether a hand-scheduled four-wave loop (CfgDma256W4, CfgDma128W4) runs
-// this problem: NN, K of at least 256, and each operand's extent (one batch)
+// this problem: K of at least 256, and each operand's extent (one batch)
 // below 2 GiB, so the loop's 32-bit buffer offsets (lane part plus K-tile
 // part) cannot wrap.
 bool dma_w4_ok(const GemmParams& p, bool ta, bool tb) {
     constexpr int64_t kLimit = int64_t(1) << 31;
-    const int64_t a_bytes = ((int64_t)(p.M - 1) * p.lda + p.K) * 4;
-    const int64_t b_bytes = ((int64_t)(p.K - 1) * p.ldb + p.N) * 4;
-    return !ta && !tb && p.K >= 256 && a_bytes < kLimit && b_bytes < kLimit;
+    const int64_t a_rows = ta ? p.K : p.M, a_cols = ta ? p.M : p.K;
+    const int64_t b_rows = tb ? p.N : p.K, b_cols = tb ? p.K : p.N;
+    const int64_t a_bytes = ((a_rows - 1) * p.lda + a_cols) * 4;
+    const int64_t b_bytes = ((b_rows - 1) * p.ldb + b_cols) * 4;
+    return p.K >= 256 && a_bytes < kLimit && b_bytes < kLimit;
 }
 
 // Launches the three-stage config One when the grid has at most one block
@@ -2251,15 +2265,15 @@ using CfgTiled128W8 = TileCfg<128, 128, 16, 32, 64, 4, 1>;
 using CfgDma256 = DmaCfg<256, 256, 16, 128, 64, 2, 1, 1>;
 // The same tile as four waves of 128x128 (one per SIMD, 256 accumulators in
 // AGPRs) with three stages and the hand-scheduled steady-state loop of
-// dma256_loop.inc: NN problems with K >= 256 whose operands span less than
-// 2 GiB (the loop's copies use 32-bit buffer offsets).  4096^3: 945 -> 915-920
+// dma_loops.inc: problems with K >= 256 whose operands span less than 2 GiB
+// (the loop's copies use 32-bit buffer offsets).  4096^3 NN: 945 -> 904-918
 // us; results bit-identical to CfgDma256 (each output adds the same products
 // in the same order).
 using CfgDma256W4 = DmaCfg<256, 256, 16, 128, 128, 3, 1, 1, 1, 4, 1, 1>;
 using CfgDma128 = DmaCfg<128, 128, 32, 64, 64, 2, 1, 1>;
 // The same tile with three stages and the hand-scheduled loop of
-// dma_loops.inc (96 KB of LDS: one block per CU), for NN problems where the
-// eight-wave 128x128 tile runs one tile per CU.
+// dma_loops.inc (96 KB of LDS: one block per CU), where the eight-wave
+// 128x128 tile would run (2048^3 NN: 130.7 -> 118-120 us).
 using CfgDma128W4 = DmaCfg<128, 128, 32, 64, 64, 3, 1, 1, 1, 4, 1, 1>;
 // 64x64x64: mid-size problems whose 128x128 tiles cannot fill the GPU.  Two
 // sets of four 32x32 waves split each K-tile's k-groups, so one block per CU

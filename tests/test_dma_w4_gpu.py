@@ -1,13 +1,14 @@
 """GPU parity of the four-wave tiles with hand-scheduled K loops (sgemm.hip's
-CfgDma256W4 and CfgDma128W4, the loops in dma_loops.inc), which run the NN
-problems FDL_KERNEL_DMA256 and FDL_KERNEL_DMA128W8 take with K >= 256.
+CfgDma256W4 and CfgDma128W4, the loops in dma_loops.inc, one per layout),
+which run the problems FDL_KERNEL_DMA256 and FDL_KERNEL_DMA128W8 take with
+K >= 256.
 
-Each output adds the same products in the same order as the eight-wave
-kernels that run the other layouts, so NN results must equal TN results (A
-stored transposed) bit for bit.  K values cover every way the asm loops hand
-over to the compiled loop: whole groups of three steady K-tiles, then zero,
-one or two more steady tiles and the checked last tiles, with and without a
-partial last K-tile."""
+Each output adds the same products in the same order whatever the layout and
+whichever form of the tile runs, so the four layouts of one product must
+agree bit for bit, and with the eight-wave form below K = 256.  K values
+cover every way the asm loops hand over to the compiled loop: whole groups of
+three steady K-tiles, then zero, one or two more steady tiles and the checked
+last tiles, with and without a partial last K-tile."""
 import numpy as np
 import pytest
 
@@ -30,39 +31,61 @@ def _rng(*key):
 
 @pytest.mark.parametrize("fam", FAMS)
 @pytest.mark.parametrize("K", KS)
-def test_w4_matches_eight_wave_bitwise(device, fam, K):
+def test_w4_layouts_agree_bitwise(device, fam, K):
     M, N = 520, 300
     g = _rng("w4", K)
     A, B = operands(g, 0, 0, M, N, K, 1)
     At = np.ascontiguousarray(np.swapaxes(A, 1, 2))
-    say(f"fam={fam} four-wave NN vs eight-wave TN, K={K}")
+    Bt = np.ascontiguousarray(np.swapaxes(B, 1, 2))
+    say(f"fam={fam} NN/NT/TN/TT, K={K}")
     c_nn = gpu_sgemm(0, 0, A, B, M, N, K, kernel=fam)
-    c_tn = gpu_sgemm(1, 0, At, B, M, N, K, kernel=fam)
-    assert np.array_equal(c_nn.view(np.uint32), c_tn.view(np.uint32))
     check_gemm(c_nn, 0, 0, A, B, M, N, K, fp32_oracle=False)
+    for ta, tb, a, b in ((0, 1, A, Bt), (1, 0, At, B), (1, 1, At, Bt)):
+        c = gpu_sgemm(ta, tb, a, b, M, N, K, kernel=fam)
+        assert np.array_equal(c_nn.view(np.uint32), c.view(np.uint32)), (ta, tb)
 
 
 @pytest.mark.parametrize("fam", FAMS)
+def test_w4_matches_eight_wave_form_bitwise(device, fam):
+    """The same product with K = 252 (the eight-wave form) and K = 256 whose
+    last four k rows of A are zero (the four-wave form): equal bit for bit,
+    since the zero products add exactly."""
+    M, N = 520, 300
+    g = _rng("w4vs8", fam)
+    A, B = operands(g, 0, 0, M, N, 256, 1)
+    A[:, :, 252:] = 0.0
+    say(f"fam={fam} K=252 eight-wave vs K=256 four-wave")
+    c8 = gpu_sgemm(0, 0, np.ascontiguousarray(A[:, :, :252]),
+                   np.ascontiguousarray(B[:, :252, :]), M, N, 252, kernel=fam)
+    c4 = gpu_sgemm(0, 0, A, B, M, N, 256, kernel=fam)
+    assert np.array_equal(c8.view(np.uint32), c4.view(np.uint32))
+
+
+@pytest.mark.parametrize("fam", FAMS)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("epi", [capi.EPILOGUE_NONE, capi.EPILOGUE_BIAS, capi.EPILOGUE_BIAS_RELU,
                                  capi.EPILOGUE_RELU])
-def test_w4_epilogues_and_batch(device, fam, epi):
+def test_w4_epilogues_and_batch(device, fam, ta, tb, epi):
     M, N, K, batch = 300, 520, 304, 3
-    g = _rng("w4e", epi)
-    A, B = operands(g, 0, 0, M, N, K, batch)
+    g = _rng("w4e", epi, ta, tb)
+    A, B = operands(g, ta, tb, M, N, K, batch)
     bias = g.standard_normal(N).astype(np.float32)
-    say(f"fam={fam} four-wave epilogue {epi}, batch {batch}")
-    c = gpu_sgemm(0, 0, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, kernel=fam)
-    check_gemm(c, 0, 0, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, fp32_oracle=False)
+    say(f"fam={fam} four-wave ta={ta} tb={tb} epilogue {epi}, batch {batch}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, kernel=fam)
+    check_gemm(c, ta, tb, A, B, M, N, K, batch=batch, bias=bias, epilogue=epi, fp32_oracle=False)
 
 
 @pytest.mark.parametrize("fam", FAMS)
-def test_w4_integer_inputs_exact(device, fam):
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_w4_integer_inputs_exact(device, fam, ta, tb):
     # Small integers: every partial sum is exact in fp32, so any order agrees.
     M, N, K = 512, 512, 1024
-    A, B = operands(_rng("w4i"), 0, 0, M, N, K, 1, dist="int")
-    say(f"fam={fam} four-wave integer inputs")
-    c = gpu_sgemm(0, 0, A, B, M, N, K, kernel=fam)
-    exact = (A[0].astype(np.float64) @ B[0].astype(np.float64))
+    A, B = operands(_rng("w4i", ta, tb), ta, tb, M, N, K, 1, dist="int")
+    say(f"fam={fam} four-wave integer inputs ta={ta} tb={tb}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, kernel=fam)
+    a = A[0].T if ta else A[0]
+    b = B[0].T if tb else B[0]
+    exact = a.astype(np.float64) @ b.astype(np.float64)
     assert np.array_equal(c[0].astype(np.float64), exact)
 
 
