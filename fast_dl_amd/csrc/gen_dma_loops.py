@@ -56,6 +56,7 @@ class Loop:
     copy_slots: tuple     # MFMAs of a group after which its copies go
     a_kc: bool = True     # A k-contiguous (not transposed)
     b_kc: bool = False    # B k-contiguous (transposed)
+    ahead: int = 1        # groups between a group's fragment reads and its MFMAs
     nt: int = 256
     stages: int = 3
 
@@ -97,9 +98,9 @@ class Loop:
 
 
 def emit(L: Loop) -> list:
-    fm, fn, ng = L.fm, L.fn, L.ng
+    fm, fn, ng, D = L.fm, L.fn, L.ng, L.ahead
     slot_regs = 4 * (fm + fn)
-    assert 160 + 2 * slot_regs <= 256
+    assert 160 + (D + 1) * slot_regs <= 256 and ng > D and (3 * ng) % (D + 1) == 0
     per_tile = L.per_a + L.per_b
     operands = {}   # read-base operand name -> C++ expression
 
@@ -167,16 +168,21 @@ def emit(L: Loop) -> list:
         out = []
         rd = list(rd)
         n = 4 * fm * fn
-        # a read every read_every MFMAs, closer where the layout has more reads
+        # a read every read_every MFMAs, closer where the layout has more
+        # reads, and several after one MFMA where a group has fewer MFMAs
         every = min(L.read_every, (n - 2) // max(1, len(rd) - 1))
-        slots = [1 + every * i for i in range(len(rd))]
+        if every > 0:
+            slots = [1 + every * i for i in range(len(rd))]
+        else:
+            slots = [1 + (i * (n - 1)) // len(rd) for i in range(len(rd))]
         assert slots[-1] < n
         last_copy = max(L.copy_slots[:len(cps)]) if cps else -1
         for j in range(n):
             q, mi, ni = j // (fm * fn), (j // fn) % fm, j % fn
             out.append(f"v_mfma_f32_32x32x2_f32 %[c{mi}{ni}], v{areg(slot, mi) + q}, "
                        f"v{breg(slot, ni) + q}, %[c{mi}{ni}]")
-            if j in slots:
+            while rd and slots and slots[0] == j:
+                slots.pop(0)
                 out.append(rd.pop(0))
             for k, cj in enumerate(L.copy_slots[:len(cps)]):
                 if cj == j:
@@ -186,16 +192,27 @@ def emit(L: Loop) -> list:
         assert not rd
         return out
 
+    reads_per_group = len(reads(0, 0, 0))
+    operands.clear()
+
     def ktile(phase):
+        # Group g's fragments were read D groups earlier into register slot
+        # (global group index) % (D + 1); during group g the wave reads group
+        # g + D, which is in tile t+1 for the last D groups.  The barrier sits
+        # before group ng - D, so those reads follow it; it waits for every
+        # read of tile t (lgkmcnt 0) and for tile t+1's copies (vmcnt).
         cur, nxt, dst = phase, (phase + 1) % 3, (phase + 2) % 3   # stages of tiles t, t+1, t+2
-        out = ["s_waitcnt lgkmcnt(0)"]                            # slot 0: group 0 of tile t
+        out = []
         for g in range(ng):
-            slot = g & 1
-            if g + 1 < ng:
-                rd = reads(slot ^ 1, g + 1, cur)
+            gg = phase * ng + g
+            if g == ng - D:
+                out += [f"s_waitcnt vmcnt({chunk_lo(ng - D)}) lgkmcnt(0)", "s_barrier"]
+            else:   # this group's fragments (reads of the D - 1 later groups may fly)
+                out.append(f"s_waitcnt lgkmcnt({min(15, (D - 1) * reads_per_group)})")
+            if g + D < ng:
+                rd = reads((gg + D) % (D + 1), g + D, cur)
             else:
-                rd = reads(slot ^ 1, 0, nxt)
-                out += [f"s_waitcnt vmcnt({chunk_lo(ng - 1)}) lgkmcnt(0)", "s_barrier"]
+                rd = reads((gg + D) % (D + 1), g + D - ng, nxt)
             ids = range(chunk_lo(g), chunk_lo(g + 1))
             cps = [copy(i, dst) for i in ids]
             advances = []
@@ -203,15 +220,14 @@ def emit(L: Loop) -> list:
                 advances.append(advance("a"))
             if per_tile - 1 in ids:
                 advances.append(advance("b"))
-            out += group(slot, rd, cps, advances)
-            if g + 2 < ng:
-                out.append("s_waitcnt lgkmcnt(0)")   # the next group's fragments
+            out += group(gg % (D + 1), rd, cps, advances)
         return out
 
     lines = ["s_mov_b32 %[m0s], m0",   # M0 is the compiler's: saved and restored
              "s_waitcnt lgkmcnt(0)",
              "s_nop 4"]                # accumulators written just before by VALU
-    lines += reads(0, 0, 0)            # group 0 of tile 0
+    for g in range(D):                 # groups 0 .. D-1 of tile 0
+        lines += reads(g, g, 0)
     label = f"L_{L.macro.lower()}_%="
     lines.append(f"{label}:")
     for phase in range(3):
@@ -243,6 +259,12 @@ for lay, (a_kc, b_kc) in LAYOUTS.items():
     # read every 2 MFMAs, a group's two copies after its first two MFMAs.
     LOOPS.append(Loop(f"FDL_DMA128W4_{lay}", 128, 128, 32, 64, 64, read_every=2,
                       copy_slots=(1, 2), a_kc=a_kc, b_kc=b_kc))
+    # 64x64x64, waves of 32x32 (CfgDma64W4): eight groups of 4 MFMAs on one
+    # accumulator (a dependent chain costs 69 cycles per MFMA against 65 for
+    # independent ones), so each group's fragments are read two groups ahead;
+    # one copy per group, after its first MFMA.
+    LOOPS.append(Loop(f"FDL_DMA64W4_{lay}", 64, 64, 64, 32, 32, read_every=1,
+                      copy_slots=(0,), a_kc=a_kc, b_kc=b_kc, ahead=2))
 
 
 def main(path):

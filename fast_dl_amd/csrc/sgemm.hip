@@ -1015,8 +1015,10 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         if constexpr (Cfg::ASM != 0) {
             static_assert(S == 3 && KS == 1 && Cfg::CW == 4 && NT == 256 &&
                               ((BM == 256 && BN == 256 && BK == 16 && FM == 4 && FN == 4) ||
-                               (BM == 128 && BN == 128 && BK == 32 && FM == 2 && FN == 2)),
-                          "the hand-scheduled loops are written for CfgDma256W4 and CfgDma128W4");
+                               (BM == 128 && BN == 128 && BK == 32 && FM == 2 && FN == 2) ||
+                               (BM == 64 && BN == 64 && BK == 64 && FM == 1 && FN == 1)),
+                          "the hand-scheduled loops are written for CfgDma256W4, CfgDma128W4 "
+                          "and CfgDma64W4");
             static_assert(OpA::PER == 4 && OpB::PER == 4, "four copies of each operand per wave");
             // Whole groups of three steady K-tiles (tile t+2 full and inside
             // K) run in the asm loop; it starts where this code stands (tiles
@@ -1109,7 +1111,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                     } else {
                         FDL_W4_LOOP(FDL_DMA256W4_TT);
                     }
-                } else {
+                } else if constexpr (BM == 128) {
                     if constexpr (!TA && !TB) {
                         FDL_W4_LOOP(FDL_DMA128W4_NN);
                     } else if constexpr (!TA) {
@@ -1118,6 +1120,16 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
                         FDL_W4_LOOP(FDL_DMA128W4_TN);
                     } else {
                         FDL_W4_LOOP(FDL_DMA128W4_TT);
+                    }
+                } else {
+                    if constexpr (!TA && !TB) {
+                        FDL_W4_LOOP(FDL_DMA64W4_NN);
+                    } else if constexpr (!TA) {
+                        FDL_W4_LOOP(FDL_DMA64W4_NT);
+                    } else if constexpr (!TB) {
+                        FDL_W4_LOOP(FDL_DMA64W4_TN);
+                    } else {
+                        FDL_W4_LOOP(FDL_DMA64W4_TT);
                     }
                 }
 #undef FDL_W4_LOOP
@@ -2284,6 +2296,9 @@ using CfgDma64 = DmaCfg<64, 64, 64, 32, 32, 2, 1, 1, 2>;
 // copies are spread over all four of its k-groups instead of the one after
 // the barrier (96 KB of LDS, so one block per CU).
 using CfgDma64S3 = DmaCfg<64, 64, 64, 32, 32, 3, 1, 1, 2>;
+// Four waves of 32x32 (one per SIMD) with the hand-scheduled loop of
+// dma_loops.inc, where the three-stage twin would run and K >= 256.
+using CfgDma64W4 = DmaCfg<64, 64, 64, 32, 32, 3, 1, 1, 1, 4, 1, 1>;
 // 128x128x64 with eight waves of 64x32 and 128 KB of LDS (one block per CU):
 // two waves per SIMD where the GPU holds about one 128x128 tile per CU
 // (2048^3: 131 vs 136.5 us for Dma128 in the same run).
@@ -2696,7 +2711,9 @@ hipError_t launch_sgemm(const GemmParams& p0, bool transA, bool transB,
                 err = launch_dma<CfgDma128>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma64:
-                err = launch_dma_fit<CfgDma64S3, CfgDma64>(p, transA, transB, nb, stream);
+                err = dma_w4_ok(p, transA, transB)
+                          ? launch_dma_fit<CfgDma64W4, CfgDma64>(p, transA, transB, nb, stream)
+                          : launch_dma_fit<CfgDma64S3, CfgDma64>(p, transA, transB, nb, stream);
                 break;
             case GemmKernel::Dma128W8:
                 err = dma_w4_ok(p, transA, transB)
