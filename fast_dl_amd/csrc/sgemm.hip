@@ -1646,6 +1646,140 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 }
 
 // ---------------------------------------------------------------------------
+// sgemm_splitk16_kernel with its operands staged in LDS by direct-to-LDS
+// copies, for the NN layout with 16-byte-aligned rows of A and B (N % 4 == 0)
+// and a K range of KC = 64 per wave (768 < K <= 1024 at KW = 16).  Wave w
+// copies the 16 x KC panel of A and the KC x 16 panel of B of its own K range
+// into its own LDS region, every copy issued at once (no registers hold the
+// bytes in flight), and waits only for its own copies.  Its MFMAs then run
+// the register kernel's sequence (same K ranges, k order and wave order of
+// the final sums), so the results are that kernel's bit for bit.
+// LDS images, per wave:
+//  * A: 16 rows of KC floats; the 16-byte chunk c of row r sits in slot
+//    c ^ kc_swz<KC / 4>(r), so a ds_read_b128 of 16 rows x one chunk spreads
+//    over the banks.
+//  * B: KC rows of 16 floats, in groups of 16 k; within a group slot row
+//    4s + q holds k = 4q + s, so the ds_read_b32 of MFMA step s (lane quarter
+//    q reads k = 4q + s) covers 64 consecutive floats.
+// Rows past M, columns past N and k past K copy clamped, in-bounds elements;
+// k past K is zeroed before its MFMA, the rest reach only unstored outputs.
+// ---------------------------------------------------------------------------
+template <int KW, int KC>
+__global__ void __launch_bounds__(KW * 64)
+sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
+    constexpr int F4 = KC / 4;            // 16-byte chunks of an A row
+    constexpr int GR = KC / 16;           // k groups of a wave
+    constexpr int A_COPIES = 16 * F4 / kWave;
+    static_assert(KC == 64, "chunk permutation and copy counts assume KC = 64");
+    __shared__ __attribute__((aligned(16))) float pan[KW][32 * KC];
+    __shared__ float red[KW][4][kWave];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int i = lane & 15;
+    const int q = lane >> 4;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * 16;
+    const int n0 = tn * 16;
+    const int64_t bz = blockIdx.y;
+    const float* __restrict__ A = p.A + bz * p.strideA;
+    const float* __restrict__ B = p.B + bz * p.strideB;
+    float* __restrict__ C = p.C + bz * p.strideC;
+    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+
+    const int kbeg = wave * KC;
+    float* as = pan[wave];
+    float* bs = pan[wave] + 16 * KC;
+    if (kbeg < p.K) {
+#pragma unroll
+        for (int t = 0; t < A_COPIES; ++t) {
+            const int e = t * kWave + lane;
+            const int r = e / F4;
+            const int c = (e % F4) ^ kc_swz<F4>(r);
+            const int64_t grow = min(m0 + r, p.M - 1);
+            const int gk = min(kbeg + 4 * c, p.K - 4);
+            dma_copy16(A + grow * p.lda + gk, as + t * 4 * kWave);
+        }
+        const int sr = lane >> 2;
+        const int kr = 4 * (sr & 3) + (sr >> 2);
+        const int gcol = min(n0 + 4 * (lane & 3), p.N - 4);
+#pragma unroll
+        for (int g = 0; g < GR; ++g) {
+            const int64_t gk = min(kbeg + 16 * g + kr, p.K - 1);
+            dma_copy16(B + gk * p.ldb + gcol, bs + g * 4 * kWave);
+        }
+    }
+    // The epilogue's elements of this thread and their extra operand, fetched
+    // while the copies fly (see epilogue_operand).
+    constexpr int kEpi = (4 * kWave + KW * kWave - 1) / (KW * kWave);
+    float pre[kEpi];
+#pragma unroll
+    for (int u = 0; u < kEpi; ++u) {
+        const int e = tid + u * KW * kWave;
+        const int r = e / kWave;
+        const int ln = e % kWave;
+        const int gi = min(m0 + 4 * (ln >> 4) + r, p.M - 1);
+        const int gj = min(n0 + (ln & 15), p.N - 1);
+        pre[u] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
+    }
+
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (kbeg < p.K) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // every fragment read issued before the first MFMA
+        floatx4 a[GR];
+        float b[GR][4];
+#pragma unroll
+        for (int g = 0; g < GR; ++g) {
+            a[g] = *reinterpret_cast<const floatx4*>(as + i * KC +
+                                                     4 * ((4 * g + q) ^ kc_swz<F4>(i)));
+#pragma unroll
+            for (int st = 0; st < 4; ++st) b[g][st] = bs[g * 4 * kWave + (4 * st + q) * 16 + i];
+        }
+#pragma unroll
+        for (int g = 0; g < GR; ++g) {
+            const int k0 = kbeg + 16 * g;
+            if (k0 >= p.K) break;
+            if (k0 + 16 > p.K) {
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const bool in = k0 + 4 * q + st < p.K;
+                    a[g][st] = in ? a[g][st] : 0.0f;
+                    b[g][st] = in ? b[g][st] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][st], b[g][st], acc, 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+
+#pragma unroll
+    for (int u = 0; u < kEpi; ++u) {
+        const int e = tid + u * KW * kWave;
+        if (e >= 4 * kWave) break;
+        const int r = e / kWave;
+        const int ln = e % kWave;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) v += red[w][r][ln];
+        const int gi = m0 + 4 * (ln >> 4) + r;
+        const int gj = n0 + (ln & 15);
+        if (gi < p.M && gj < p.N) {
+            store_epilogue_pre(v, p, C, upd, (int64_t)gi * p.ldc + gj, pre[u]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny kernel for M <= MR (MR <= 8) with B not transposed: a bandwidth
 // kernel whose cost is one pass over B.  A block of NT threads owns a strip of
 // STRIP columns and the whole K range: CL lanes across the strip (float4 each
@@ -2172,6 +2306,13 @@ hipError_t launch_splitk16_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
 // K = 512, 8 from 128, else 4; one group in flight per buffer).
 hipError_t launch_splitk16(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                            int nbatch, hipStream_t stream) {
+    // NN with 16-byte rows and 64 k per wave: the LDS-staged form.
+    if (!ta && !tb && va && vb && p.K > 768 && p.K <= 1024) {
+        const dim3 grid(((p.M + 15) / 16) * ((p.N + 15) / 16), nbatch);
+        hipLaunchKernelGGL((sgemm_splitk16_lds_kernel<16, 64>), grid, dim3(16 * kWave), 0, stream,
+                           p, (p.M + 15) / 16, (p.N + 15) / 16);
+        return hipGetLastError();
+    }
     if (p.K >= 512) return launch_splitk16_kw<16, 1>(p, ta, tb, va, vb, nbatch, stream);
     if (p.K >= 128) return launch_splitk16_kw<8, 1>(p, ta, tb, va, vb, nbatch, stream);
     return launch_splitk16_kw<4, 1>(p, ta, tb, va, vb, nbatch, stream);

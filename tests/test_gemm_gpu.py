@@ -13,7 +13,7 @@ import pytest
 import fast_dl_amd.capi as capi
 import oracle
 from tests.conftest import rng
-from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, say, stream
+from tests.gpu_helpers import check_gemm, dev, gpu_sgemm, host, operands, say, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -273,3 +273,39 @@ def test_kernel_choice_heuristic(device):
     assert capi.kernel_choice(0, 0, 4096, 4096, 4096) == capi.KERNEL_DMA256
     assert capi.kernel_choice(0, 0, 1, 4096, 4096) == capi.KERNEL_SKINNY
     assert capi.kernel_choice(0, 1, 1, 4096, 4096) != capi.KERNEL_SKINNY
+
+
+# NN problems with 768 < K <= 1024 and 16-byte rows take the splitk16 form
+# that stages each wave's K range in LDS (C1 and the MLP forward are such
+# problems).  The same operands with a row pitch that is not a multiple of 4
+# floats take the register form, whose k order and wave order it keeps.
+@pytest.mark.parametrize("M,N,K,batch,epi", [
+    (256, 128, 784, 1, capi.EPILOGUE_NONE),
+    (256, 256, 784, 1, capi.EPILOGUE_BIAS_RELU),
+    (33, 20, 772, 1, capi.EPILOGUE_BIAS),
+    (17, 44, 1024, 3, capi.EPILOGUE_RELU),
+    (130, 36, 1000, 1, capi.EPILOGUE_RELU_GRAD),
+    (16, 16, 788, 2, capi.EPILOGUE_NONE),
+])
+def test_splitk16_lds_staged(device, M, N, K, batch, epi):
+    g = rng(M * 131 + N * 17 + K)
+    A, B = operands(g, 0, 0, M, N, K, batch)
+    bias = (g.standard_normal(N) * 0.1).astype(np.float32)
+    aux = (g.standard_normal((batch, M, N)).astype(np.float32)
+           if epi == capi.EPILOGUE_RELU_GRAD else None)
+    say(f"splitk16 LDS-staged M={M} N={N} K={K} batch={batch} epi={epi}")
+    c = gpu_sgemm(0, 0, A, B, M, N, K, batch=batch, bias=bias, aux=aux, epilogue=epi,
+                  kernel=capi.KERNEL_SPLITK16)
+    check_gemm(c, 0, 0, A, B, M, N, K, batch=batch, bias=bias, aux=aux, epilogue=epi,
+               fp32_oracle=True)
+    # the register form on the same values (row pitch K + 1): the same bits
+    A_pad = np.zeros((batch, M, K + 1), np.float32)
+    A_pad[:, :, :K] = A
+    c_reg = gpu_sgemm(0, 0, A_pad, B, M, N, K, batch=batch, bias=bias, aux=aux, epilogue=epi,
+                      kernel=capi.KERNEL_SPLITK16, lda=K + 1)
+    assert np.array_equal(c, c_reg)
+    # integer operands: every order exact
+    Ai, Bi = operands(g, 0, 0, M, N, K, batch, dist="int")
+    ci = gpu_sgemm(0, 0, Ai, Bi, M, N, K, batch=batch, kernel=capi.KERNEL_SPLITK16)
+    exact = np.einsum("bmk,bkn->bmn", Ai.astype(np.int64), Bi.astype(np.int64))
+    assert np.array_equal(ci, exact.astype(np.float32))
