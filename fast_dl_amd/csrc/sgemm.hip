@@ -1663,6 +1663,8 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 //    q reads k = 4q + s) covers 64 consecutive floats.
 // Rows past M, columns past N and k past K copy clamped, in-bounds elements;
 // k past K is zeroed before its MFMA, the rest reach only unstored outputs.
+// The block has one wave per KC of K (at most KW); the register form's idle
+// waves only added +0.0 to each sum, so the results are still its bits.
 // ---------------------------------------------------------------------------
 template <int KW, int KC>
 __global__ void __launch_bounds__(KW * 64)
@@ -1691,6 +1693,7 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
     float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
 
+    const int nw = blockDim.x / kWave;
     const int kbeg = wave * KC;
     float* as = pan[wave];
     float* bs = pan[wave] + 16 * KC;
@@ -1715,11 +1718,12 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
     }
     // The epilogue's elements of this thread and their extra operand, fetched
     // while the copies fly (see epilogue_operand).
-    constexpr int kEpi = (4 * kWave + KW * kWave - 1) / (KW * kWave);
+    // nw >= 4 (K > 768), so one element per thread of the first four waves
+    constexpr int kEpi = 1;
     float pre[kEpi];
 #pragma unroll
     for (int u = 0; u < kEpi; ++u) {
-        const int e = tid + u * KW * kWave;
+        const int e = tid;
         const int r = e / kWave;
         const int ln = e % kWave;
         const int gi = min(m0 + 4 * (ln >> 4) + r, p.M - 1);
@@ -1764,13 +1768,12 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
 
 #pragma unroll
     for (int u = 0; u < kEpi; ++u) {
-        const int e = tid + u * KW * kWave;
+        const int e = tid;
         if (e >= 4 * kWave) break;
         const int r = e / kWave;
         const int ln = e % kWave;
         float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < KW; ++w) v += red[w][r][ln];
+        for (int w = 0; w < nw; ++w) v += red[w][r][ln];
         const int gi = m0 + 4 * (ln >> 4) + r;
         const int gj = n0 + (ln & 15);
         if (gi < p.M && gj < p.N) {
@@ -2309,8 +2312,9 @@ hipError_t launch_splitk16(const GemmParams& p, bool ta, bool tb, bool va, bool 
     // NN with 16-byte rows and 64 k per wave: the LDS-staged form.
     if (!ta && !tb && va && vb && p.K > 768 && p.K <= 1024) {
         const dim3 grid(((p.M + 15) / 16) * ((p.N + 15) / 16), nbatch);
-        hipLaunchKernelGGL((sgemm_splitk16_lds_kernel<16, 64>), grid, dim3(16 * kWave), 0, stream,
-                           p, (p.M + 15) / 16, (p.N + 15) / 16);
+        const int waves = (p.K + 63) / 64;  // 13 to 16
+        hipLaunchKernelGGL((sgemm_splitk16_lds_kernel<16, 64>), grid, dim3(waves * kWave), 0,
+                           stream, p, (p.M + 15) / 16, (p.N + 15) / 16);
         return hipGetLastError();
     }
     if (p.K >= 512) return launch_splitk16_kw<16, 1>(p, ta, tb, va, vb, nbatch, stream);
