@@ -1655,13 +1655,14 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 // and a K range of KC = 64 per wave (768 < K <= 1024 at KW = 16).  Wave w
 // copies the 16 x KC panel of A and the KC x 16 panel of B of its own K range
 // into its own LDS region, every copy issued at once (no registers hold the
-// bytes in flight), and waits only for its own copies.  Its MFMAs then run
+// bytes in flight), and waits only for its own copies, a 16-k group at a
+// time (the MFMAs of a group run while later groups land).  Its MFMAs run
 // the register kernel's sequence (same K ranges, k order and wave order of
 // the final sums), so the results are that kernel's bit for bit.
 // LDS images, per wave:
-//  * A: 16 rows of KC floats; the 16-byte chunk c of row r sits in slot
-//    c ^ kc_swz<KC / 4>(r), so a ds_read_b128 of 16 rows x one chunk spreads
-//    over the banks.
+//  * A: group-major, GR groups of 16 rows x 16 k (one 1 KB copy each); in a
+//    group the 16-byte chunk c of row r sits in slot c ^ kc_swz<4>(r), so a
+//    ds_read_b128 of 16 rows x one chunk spreads over the banks.
 //  * B: KC rows of 16 floats, in groups of 16 k; within a group slot row
 //    4s + q holds k = 4q + s, so the ds_read_b32 of MFMA step s (lane quarter
 //    q reads k = 4q + s) covers 64 consecutive floats.
@@ -1673,11 +1674,15 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 template <int KW, int KC>
 __global__ void __launch_bounds__(KW * 64)
 sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
-    constexpr int F4 = KC / 4;            // 16-byte chunks of an A row
     constexpr int GR = KC / 16;           // k groups of a wave
-    constexpr int A_COPIES = 16 * F4 / kWave;
-    static_assert(KC == 64, "chunk permutation and copy counts assume KC = 64");
-    __shared__ __attribute__((aligned(16))) float pan[KW][32 * KC];
+    static_assert(KC == 64 && GR == 4, "copy counts and waits assume KC = 64 (four groups)");
+    // One array per k group (A's 16 x 16 floats, then B's 16 x 16), so that
+    // the compiler sees a group's reads alias only that group's copies and
+    // waits for those alone (with one array it waits for every copy).
+    __shared__ __attribute__((aligned(16))) float lg0[KW][512];
+    __shared__ __attribute__((aligned(16))) float lg1[KW][512];
+    __shared__ __attribute__((aligned(16))) float lg2[KW][512];
+    __shared__ __attribute__((aligned(16))) float lg3[KW][512];
     __shared__ float red[KW][4][kWave];
 
     const int tid = threadIdx.x;
@@ -1697,32 +1702,10 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
     const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
     float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
 
-    const int nw = blockDim.x / kWave;
-    const int kbeg = wave * KC;
-    float* as = pan[wave];
-    float* bs = pan[wave] + 16 * KC;
-    if (kbeg < p.K) {
-#pragma unroll
-        for (int t = 0; t < A_COPIES; ++t) {
-            const int e = t * kWave + lane;
-            const int r = e / F4;
-            const int c = (e % F4) ^ kc_swz<F4>(r);
-            const int64_t grow = min(m0 + r, p.M - 1);
-            const int gk = min(kbeg + 4 * c, p.K - 4);
-            dma_copy16(A + grow * p.lda + gk, as + t * 4 * kWave);
-        }
-        const int sr = lane >> 2;
-        const int kr = 4 * (sr & 3) + (sr >> 2);
-        const int gcol = min(n0 + 4 * (lane & 3), p.N - 4);
-#pragma unroll
-        for (int g = 0; g < GR; ++g) {
-            const int64_t gk = min(kbeg + 16 * g + kr, p.K - 1);
-            dma_copy16(B + gk * p.ldb + gcol, bs + g * 4 * kWave);
-        }
-    }
-    // The epilogue's elements of this thread and their extra operand, fetched
-    // while the copies fly (see epilogue_operand).
-    // nw >= 4 (K > 768), so one element per thread of the first four waves
+    // The epilogue's elements of this thread and their extra operand
+    // (see epilogue_operand), loaded first so that the copies' waits below
+    // count copies only.  nw >= 4 (K > 768): one element per thread of the
+    // first four waves.
     constexpr int kEpi = 1;
     float pre[kEpi];
 #pragma unroll
@@ -1735,35 +1718,74 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
         pre[u] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
     }
 
+    const int nw = blockDim.x / kWave;
+    const int kbeg = wave * KC;
+    auto region = [&](auto gc) -> float* {
+        constexpr int g = decltype(gc)::value;
+        if constexpr (g == 0) return lg0[wave];
+        else if constexpr (g == 1) return lg1[wave];
+        else if constexpr (g == 2) return lg2[wave];
+        else return lg3[wave];
+    };
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (kbeg < p.K) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        // every fragment read issued before the first MFMA
-        floatx4 a[GR];
-        float b[GR][4];
-#pragma unroll
-        for (int g = 0; g < GR; ++g) {
-            a[g] = *reinterpret_cast<const floatx4*>(as + i * KC +
-                                                     4 * ((4 * g + q) ^ kc_swz<F4>(i)));
-#pragma unroll
-            for (int st = 0; st < 4; ++st) b[g][st] = bs[g * 4 * kWave + (4 * st + q) * 16 + i];
-        }
-#pragma unroll
-        for (int g = 0; g < GR; ++g) {
+        // Copies in group order, A's then B's of each group, so group g has
+        // landed once at most 2 (GR - 1 - g) copies are outstanding.
+        const int ar = lane >> 2;             // A: row of this lane's chunk
+        const int aq = lane & 3;              // A: slot within the row's group
+        const int ac = aq ^ kc_swz<4>(ar);    // A: the chunk (k / 4 in the group) it holds
+        const int arow = min(m0 + ar, p.M - 1) - m0;
+        const int sr = lane >> 2;             // B: slot row of the group
+        const int kr = 4 * (sr & 3) + (sr >> 2);
+        const int bcol = min(n0 + 4 * (lane & 3), p.N - 4) - n0;
+        // Buffer copies from wave-uniform bases (the block's first row of A,
+        // the wave's first k row of B); the lane parts are 32-bit offsets
+        // (the host keeps 16 rows of A and 64 rows of B below 2 GiB).
+        const __amdgpu_buffer_rsrc_t ra = dma_buffer(wave_uniform(A + (int64_t)m0 * p.lda));
+        const __amdgpu_buffer_rsrc_t rb =
+            dma_buffer(wave_uniform(B + (int64_t)kbeg * p.ldb + n0));
+        auto copy = [&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const int gk = min(kbeg + 16 * g + 4 * ac, p.K - 4);
+            dma_buf_copy16(ra, (uint32_t)((int64_t)arow * p.lda + gk) * 4u, region(gc));
+            const int bk = min(kbeg + 16 * g + kr, p.K - 1) - kbeg;
+            dma_buf_copy16(rb, (uint32_t)((int64_t)bk * p.ldb + bcol) * 4u,
+                           region(gc) + 4 * kWave);
+        };
+        copy(std::integral_constant<int, 0>{});
+        copy(std::integral_constant<int, 1>{});
+        copy(std::integral_constant<int, 2>{});
+        copy(std::integral_constant<int, 3>{});
+        // Group g's MFMAs start as soon as its two copies have landed: the
+        // compiler, which must wait for a direct-to-LDS copy before reading
+        // what it wrote, tells the four arrays apart and waits for
+        // vmcnt(2 (GR - 1 - g)) before group g's reads (checked in the ISA).
+        auto group = [&](auto gc) {
+            constexpr int g = decltype(gc)::value;
             const int k0 = kbeg + 16 * g;
-            if (k0 >= p.K) break;
+            if (k0 >= p.K) return;
+            const float* as = region(gc);
+            const float* bs = as + 4 * kWave;
+            floatx4 a = *reinterpret_cast<const floatx4*>(as + i * 16 + 4 * (q ^ kc_swz<4>(i)));
+            float b[4];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) b[st] = bs[(4 * st + q) * 16 + i];
             if (k0 + 16 > p.K) {
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
                     const bool in = k0 + 4 * q + st < p.K;
-                    a[g][st] = in ? a[g][st] : 0.0f;
-                    b[g][st] = in ? b[g][st] : 0.0f;
+                    a[st] = in ? a[st] : 0.0f;
+                    b[st] = in ? b[st] : 0.0f;
                 }
             }
 #pragma unroll
             for (int st = 0; st < 4; ++st)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][st], b[g][st], acc, 0, 0, 0);
-        }
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b[st], acc, 0, 0, 0);
+        };
+        group(std::integral_constant<int, 0>{});
+        group(std::integral_constant<int, 1>{});
+        group(std::integral_constant<int, 2>{});
+        group(std::integral_constant<int, 3>{});
     }
 
 #pragma unroll
@@ -2313,8 +2335,10 @@ hipError_t launch_splitk16_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
 // K = 512, 8 from 128, else 4; one group in flight per buffer).
 hipError_t launch_splitk16(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                            int nbatch, hipStream_t stream) {
-    // NN with 16-byte rows and 64 k per wave: the LDS-staged form.
-    if (!ta && !tb && va && vb && p.K > 768 && p.K <= 1024) {
+    // NN with 16-byte rows and 64 k per wave: the LDS-staged form (its
+    // 32-bit copy offsets span 16 rows of A and 64 rows of B).
+    if (!ta && !tb && va && vb && p.K > 768 && p.K <= 1024 && p.lda < (int64_t(1) << 24) &&
+        p.ldb < (int64_t(1) << 22)) {
         const dim3 grid(((p.M + 15) / 16) * ((p.N + 15) / 16), nbatch);
         const int waves = (p.K + 63) / 64;  // 13 to 16
         hipLaunchKernelGGL((sgemm_splitk16_lds_kernel<16, 64>), grid, dim3(waves * kWave), 0,
