@@ -60,6 +60,7 @@ SIGNATURES = {
                                      _vp, _vp, _vp, _vp, _vp]),
     "fdl_mlp2_graph_launch": (_int, [_vp, _vp]),
     "fdl_mlp2_graph_destroy": (_int, [_vp]),
+    "fdl_zero_fill": (_int, [_vp, _i64, _vp]),
     "fdl_fill_uniform": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
     "fdl_fill_normal": (_int, [_vp, _i64, _flt, _flt, ctypes.c_uint64, _vp]),
     "fdl_idx_gather": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _flt, _vp, _vp, _vp]),

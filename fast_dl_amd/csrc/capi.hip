@@ -575,6 +575,14 @@ int fdl_mlp2_graph_destroy(fdl_mlp2_graph* g) {
     return check_hip(e2, "mlp2_graph_destroy");
 }
 
+int fdl_zero_fill(void* data, int64_t bytes, void* stream) {
+    if (bytes < 0) return fail(FDL_ERROR_INVALID_VALUE, "zero_fill: negative size");
+    if (bytes == 0) return FDL_SUCCESS;
+    if (!data) return fail(FDL_ERROR_INVALID_VALUE, "zero_fill: null pointer");
+    return check_hip(fdl::launch_zero_fill(data, bytes, as_stream(stream)),
+                     "zero_fill launch failed");
+}
+
 int fdl_fill_uniform(float* data, int64_t n, float low, float high, uint64_t seed,
                      void* stream) {
     if (n < 0) return fail(FDL_ERROR_INVALID_VALUE, "fill_uniform: negative size");

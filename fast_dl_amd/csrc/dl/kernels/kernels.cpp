@@ -44,6 +44,10 @@ namespace dl::kernels {
 
 const char* to_string(GemmAlgo algo) {
     switch (algo) {
+        case GemmAlgo::Naive: return "naive";
+        case GemmAlgo::Tiled: return "tiled";
+        case GemmAlgo::Register: return "register";
+        case GemmAlgo::Cublas: return "cublas";
         case GemmAlgo::Auto: return "auto";
         case GemmAlgo::MfmaTiled128: return "mfma_tiled128";
         case GemmAlgo::MfmaTiled64: return "mfma_tiled64";
@@ -65,6 +69,10 @@ namespace {
 
 int kernel_id(GemmAlgo algo) {
     switch (algo) {
+        case GemmAlgo::Naive: return FDL_KERNEL_SPLITK32;
+        case GemmAlgo::Tiled: return FDL_KERNEL_TILED64;
+        case GemmAlgo::Register: return FDL_KERNEL_TILED128;
+        case GemmAlgo::Cublas: return FDL_KERNEL_AUTO;
         case GemmAlgo::Auto: return FDL_KERNEL_AUTO;
         case GemmAlgo::MfmaTiled128: return FDL_KERNEL_TILED128;
         case GemmAlgo::MfmaTiled64: return FDL_KERNEL_TILED64;
@@ -107,7 +115,8 @@ void gemm_ex(Transpose trans_a, Transpose trans_b, int64_t m, int64_t n, int64_t
              void* stream) {
     const int ta = trans_a == Transpose::Yes ? FDL_OP_T : FDL_OP_N;
     const int tb = trans_b == Transpose::Yes ? FDL_OP_T : FDL_OP_N;
-    if (algo == GemmAlgo::Auto) {
+    // Cublas named the reference's production path; here that is the automatic choice.
+    if (algo == GemmAlgo::Auto || algo == GemmAlgo::Cublas) {
         hip::check_fdl(detail::sgemm_auto(ta, tb, m, n, k, a, lda, stride_a, b, ldb, stride_b, c,
                                           ldc, stride_c, batch, bias, aux, epilogue_id(epilogue),
                                           stream),

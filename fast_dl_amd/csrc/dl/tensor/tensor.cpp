@@ -16,6 +16,7 @@
 #include <dl/kernels/random.hpp>
 #include <dl/tensor/Tensor.hpp>
 #include <dl/tensor/TensorImpl.hpp>
+#include <fastdl_gemm.h>
 
 #include <hip/hip_runtime_api.h>
 
@@ -205,8 +206,8 @@ void TensorImpl::note_use() const {
 }
 
 void TensorImpl::record_stream(void* stream) const {
-    if (stream == stream_ || std::find(uses_.begin(), uses_.end(), stream) != uses_.end()) return;
-    uses_.push_back(stream);
+    // stream_ is fixed from allocation on; only uses on other streams are listed
+    if (stream != stream_) uses_.record(stream);
 }
 const Shape& TensorImpl::shape() const { return shape_; }
 DType TensorImpl::dtype() const { return dtype_; }
@@ -226,10 +227,11 @@ void TensorImpl::allocate() {
 void TensorImpl::release() {
     if (!data_) return;
     if (device_.is_cuda()) {
-        detail::device_block_cache().release(device_.index, nbytes(), data_, stream_, uses_);
+        detail::device_block_cache().release(device_.index, nbytes(), data_, stream_,
+                                             uses_.take());
     }
     data_ = nullptr;
-    uses_.clear();
+    uses_.take();
 }
 
 void TensorImpl::copy_from_host(const void* src, std::size_t bytes) {
@@ -291,12 +293,11 @@ void TensorImpl::zero_() {
     if (!device_.is_cuda()) throw std::runtime_error("zero_ currently supports CUDA tensors only");
     hip::check(hipSetDevice(device_.index), "cudaSetDevice failed");
     note_use();
-    const hipStream_t s = static_cast<hipStream_t>(current_stream());
-    if (s) {
-        hip::check(hipMemsetAsync(data_, 0, nbytes(), s), "cudaMemset failed");
-    } else {
-        hip::check(hipMemset(data_, 0, nbytes()), "cudaMemset failed");
-    }
+    // A kernel on the current stream, not hipMemsetAsync: zeros() and
+    // Linear's bias stay capturable into a graph (a captured memset node
+    // gave wrong results on replays).
+    hip::check_fdl(fdl_zero_fill(data_, static_cast<int64_t>(nbytes()), current_stream()),
+                   "cudaMemset failed");
 }
 
 // -------------------------------------------------------------------- Tensor

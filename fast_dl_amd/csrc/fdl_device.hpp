@@ -9,6 +9,15 @@
 
 namespace fdl {
 
+// Waits until no vector-memory operation of this wave is outstanding
+// (s_waitcnt vmcnt(0), lgkmcnt and expcnt unconstrained).  Placed before a
+// run of stores whose values use operands loaded early: where the compiler
+// cannot prove those loads have landed (a path that skips the main loop
+// merges in), it waits for them before each store, and since stores count in
+// vmcnt with the loads, each of those waits also waits for the stores just
+// issued.  On the main path nothing is outstanding here, so this costs nothing.
+__device__ __forceinline__ void wait_vmem_idle() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Column sums of a row-major rows x cols matrix, 32 columns per block and 8
 // row groups per column (256 threads).  Row groups are added in group order,
 // so the result is deterministic.  With `param`, the block also applies
@@ -26,6 +35,11 @@ __device__ __forceinline__ void colsum_body(const float* __restrict__ x, float* 
     const int grp = threadIdx.x / kColsumCols;
     const int64_t c = block * (int64_t)kColsumCols + cl;
     const int64_t cc = c < cols ? c : cols - 1;  // clamped: loads stay in bounds
+    // The parameter's value, fetched now (`param` is the same on every lane, so
+    // this is a scalar branch): loaded after the sums it costs a second round
+    // trip to memory at the end of the block.
+    float pv = 0.0f;
+    if (param) pv = param[cc];
     // Rows are added in order (grp, grp + 8, grp + 16, ...); the loads of
     // 32 of them are in flight at once, so a 256-row matrix costs one
     // round trip to memory instead of four.
@@ -52,11 +66,11 @@ __device__ __forceinline__ void colsum_body(const float* __restrict__ x, float* 
         float t = part[0][cl];
 #pragma unroll
         for (int g = 1; g < kColsumGroups; ++g) t += part[g][cl];
+        const float step = lr * t;
+        const float np = pv - step;
+        wait_vmem_idle();
         out[c] = t;
-        if (param) {
-            const float step = lr * t;
-            param[c] = param[c] - step;
-        }
+        if (param) param[c] = np;
     }
 }
 
@@ -100,15 +114,17 @@ __device__ __forceinline__ void xent_finalize_body(const float* __restrict__ par
 }
 
 // The MLP head's reductions from its stored outputs (one block of 256
-// threads, classes <= kColsumCols): db = column sums of G (colsum_body, with
-// the bias step bparam -= lr * db), and the loss, each row's share
-// (logf(sum_c expf(z_c - max)) + max - z_label) / rows computed from its
-// stored logits z as the head computes it (classes in order; rows with a
-// label outside [0, classes) add nothing).  A thread takes rows t, t + 256,
-// ...; a row's logits and label are loaded before the column sums (all
-// kColsumCols loads at clamped addresses, so none waits on another), the
-// shares are summed in row order per thread, then over each wave by a fixed
-// exchange tree and over the waves in order.
+// threads, classes <= kColsumCols): db = column sums of G with the bias step
+// bparam -= lr * db (the sums and their order exactly as colsum_body's), and
+// the loss, each row's share (logf(sum_c expf(z_c - max)) + max - z_label) /
+// rows computed from its stored logits z as the head computes it (classes in
+// order; rows with a label outside [0, classes) add nothing).  A thread takes
+// rows t, t + 256, ... for the loss; the shares are summed in row order per
+// thread, then over each wave by a fixed exchange tree and over the waves in
+// order.  Every load of the first 256 rows (the row's logits and label, the
+// bias, and 32 rows of G per thread for the column sums, at clamped
+// addresses) is issued before any is used, so the loss is computed while the
+// column sums' rows are still arriving.
 template <int CM>
 __device__ __forceinline__ void head_finalize_body(const float* __restrict__ logits,
                                                    const float* __restrict__ g,
@@ -117,19 +133,30 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
                                                    float* __restrict__ loss,
                                                    float* __restrict__ db,
                                                    float* __restrict__ bparam, float lr) {
+#pragma clang fp contract(off)
     static_assert(CM <= kColsumCols, "one block of column sums");
+    __shared__ float part[kColsumGroups][kColsumCols];
+    __shared__ float wpart[kColsumThreads / 64];
+    constexpr int kFirst = 32;  // column-sum rows per thread issued up front
     const int t = threadIdx.x;
+    const int cl = t % kColsumCols;
+    const int grp = t / kColsumCols;
+    const int64_t cc = cl < classes ? cl : classes - 1;
     const int64_t r0 = t < rows ? t : rows - 1;
     float z[CM];
 #pragma unroll
     for (int c = 0; c < CM; ++c) z[c] = logits[r0 * classes + (c < classes ? c : classes - 1)];
     const int64_t label0 = labels[r0];
-    colsum_body(g, db, bparam, lr, rows, classes, 0);
-    if (!loss) return;
-    __shared__ float wpart[kColsumThreads / 64];
+    const float pv = bparam ? bparam[cc] : 0.0f;
+    float gv[kFirst];
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u) {
+        const int64_t r = grp + (int64_t)u * kColsumGroups;
+        gv[u] = g[(r < rows ? r : rows - 1) * classes + cc];
+    }
+
     float s = 0.0f;
-    {
-#pragma clang fp contract(off)
+    if (loss) {
         const float inv_b = 1.0f / (float)rows;
         for (int64_t r = t; r < rows; r += kColsumThreads) {
             int64_t label = label0;
@@ -159,10 +186,43 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     }
+
+    // Column sums, rows grp, grp + 8, ... in order (colsum_body's order).
+    float cs = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u) {
+        if (grp + (int64_t)u * kColsumGroups < rows) cs += gv[u];
+    }
+    int64_t r = grp + (int64_t)kFirst * kColsumGroups;
+    for (; r + 31 * kColsumGroups < rows; r += 32 * kColsumGroups) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = g[(r + u * kColsumGroups) * classes + cc];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) cs += v[u];
+    }
+    for (; r + 7 * kColsumGroups < rows; r += 8 * kColsumGroups) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = g[(r + u * kColsumGroups) * classes + cc];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cs += v[u];
+    }
+    for (; r < rows; r += kColsumGroups) cs += g[r * classes + cc];
+    part[grp][cl] = cs;
     if ((t & 63) == 0) wpart[t >> 6] = s;
     __syncthreads();
-    if (t == 0) {
-#pragma clang fp contract(off)
+    if (grp == 0 && cl < classes) {
+        float tsum = part[0][cl];
+#pragma unroll
+        for (int q = 1; q < kColsumGroups; ++q) tsum += part[q][cl];
+        const float step = lr * tsum;
+        const float np = pv - step;
+        wait_vmem_idle();
+        db[cl] = tsum;
+        if (bparam) bparam[cl] = np;
+    }
+    if (t == 0 && loss) {
         float l = wpart[0];
 #pragma unroll
         for (int i = 1; i < kColsumThreads / 64; ++i) l += wpart[i];

@@ -197,6 +197,8 @@ hipError_t launch_sgd(float* param, const float* grad, float lr, int64_t n,
 hipError_t launch_sgd_multi(int count, float* const* params,
                             const float* const* grads, const int64_t* sizes,
                             float lr, hipStream_t stream);
+// data[0 .. bytes) = 0 by a kernel (capturable, unlike a memset node).
+hipError_t launch_zero_fill(void* data, int64_t bytes, hipStream_t stream);
 hipError_t launch_fill_uniform(float* data, int64_t n, float low, float high,
                                uint64_t seed, hipStream_t stream);
 hipError_t launch_fill_normal(float* data, int64_t n, float mean, float stddev,

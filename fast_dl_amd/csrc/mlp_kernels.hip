@@ -736,6 +736,19 @@ __global__ void sgd_multi_kernel(SgdMulti args, float lr) {
     }
 }
 
+// data[0 .. bytes) = 0: 16-byte stores over the aligned body, byte stores at
+// the ends.  A kernel rather than hipMemsetAsync, so that a caller may capture
+// it into a graph (a captured memset node gave wrong results on replays).
+__global__ void zero_fill_kernel(unsigned char* __restrict__ data, int64_t head, int64_t n16,
+                                 int64_t tail) {
+    const int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    uint4* body = reinterpret_cast<uint4*>(data + head);
+    for (int64_t e = i; e < n16; e += stride) body[e] = make_uint4(0u, 0u, 0u, 0u);
+    if (i < head) data[i] = 0;
+    if (i < tail) data[head + 16 * n16 + i] = 0;
+}
+
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
 // easy as 1, 2, 3", SC'11): counter (i_lo, i_hi, 0, 0), key = seed.
 struct Philox4 {
@@ -934,6 +947,17 @@ hipError_t launch_sgd_multi(int count, float* const* params,
     if (nmax == 0) return hipSuccess;
     hipLaunchKernelGGL(sgd_multi_kernel, dim3(grid_for(nmax, 4), count),
                        dim3(kBlock), 0, stream, args, lr);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_fill(void* data, int64_t bytes, hipStream_t stream) {
+    auto* p = static_cast<unsigned char*>(data);
+    const int64_t head = std::min<int64_t>((16 - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u,
+                                           bytes);
+    const int64_t n16 = (bytes - head) / 16;
+    const int64_t tail = bytes - head - 16 * n16;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(std::max(1u, grid_for(n16, 4))), dim3(kBlock), 0,
+                       stream, p, head, n16, tail);
     return hipGetLastError();
 }
 

@@ -145,8 +145,15 @@ def collect(out_dir: str, stages: list[str], configs: list[str] | None = None) -
         argv = ["timeout", "-s", "KILL", "150", "rocprofv3", *prof_args, "--output-format", "csv",
                 "-d", os.path.join(out_dir, name), "-o", "run", "--",
                 *_bench_argv(cfg, vendor=vendor, pmc=pmc)]
-        rc = _run(argv, os.path.join(out_dir, name + ".log"))
-        ok = rc == 0 or (rc == 139 and _has_results(os.path.join(out_dir, name)))
+        log = os.path.join(out_dir, name + ".log")
+        rc = _run(argv, log)
+        # rocprofv3 itself can end with SIGSEGV (139) after the profiled program
+        # has finished and its output files are written (seen at the tool's
+        # teardown on this stack).  Such a pass counts only if the program
+        # printed its closing profile_mode line and the CSV holds at least the
+        # timed dispatches.
+        ok = rc == 0 or (rc == 139 and _finished(log) and
+                         _dispatches(os.path.join(out_dir, name)) >= CONFIGS[cfg].steps)
         print(f"[{i + 1}/{len(jobs)}] {name}: rc={rc} {time.time() - t0:.1f}s", flush=True)
         if not ok:
             print(f"stopping: {name} failed (see {name}.log)", flush=True)
@@ -154,8 +161,27 @@ def collect(out_dir: str, stages: list[str], configs: list[str] | None = None) -
     return 0
 
 
-def _has_results(d: str) -> bool:
-    return bool(glob.glob(os.path.join(d, "**", "*.csv"), recursive=True))
+def _finished(log: str) -> bool:
+    """Whether the profiled bench.py printed its closing {"profile_mode": true, ...} line."""
+    try:
+        with open(log) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return False
+    for line in reversed(lines):
+        if line.startswith("{") and '"profile_mode": true' in line:
+            return True
+    return False
+
+
+def _dispatches(d: str) -> int:
+    """Rows of the pass's kernel trace or counter CSV (0 when there is none)."""
+    for suffix in ("kernel_trace.csv", "counter_collection.csv"):
+        files = glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)
+        if files:
+            with open(files[0]) as f:
+                return max(0, sum(1 for _ in f) - 1)
+    return 0
 
 
 # ------------------------------------------------------------------- reading CSV

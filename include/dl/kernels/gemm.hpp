@@ -4,9 +4,13 @@
 // gemm() keeps the reference's signature and contract: row-major
 // C[m,n] = A[m,k] . B[k,n], C overwritten, enqueued on the calling thread's
 // current stream (dl/core/Stream.hpp; the null stream unless the caller
-// chose another, as in the reference).  The GemmAlgo
-// enumerators name this build's gfx950 kernel families; Auto (the default)
-// picks one by shape, as the reference's default picked cuBLAS.
+// chose another, as in the reference).  GemmAlgo keeps the reference's four
+// enumerators (include/dl/kernels/gemm.hpp:7-12 there; src/ops/Matmul.cpp:42
+// and tests/benchmarks/gemm/gemm_benchmark.cu:87-99 name them), each mapped
+// to the gfx950 family closest to the kernel it named; Cublas, the
+// reference's production path, is the automatic choice.  The remaining
+// enumerators name this build's kernel families; Auto (the default) picks
+// one by shape, as the reference's default picked cuBLAS.
 
 #include <cstddef>
 #include <cstdint>
@@ -14,6 +18,11 @@
 namespace dl::kernels {
 
 enum class GemmAlgo {
+    Naive,          // reference: direct K loop, no shared memory -> MfmaSplitK (operands
+                    // straight from L2 into MFMA registers)
+    Tiled,          // reference: 16x16 shared-memory tiles -> MfmaTiled64
+    Register,       // reference: 128x128 block tile, register blocking -> MfmaTiled128
+    Cublas,         // reference: cublasSgemm, the production path -> Auto
     Auto,
     MfmaTiled128,   // 128x128x16 LDS double-buffered fp32 MFMA tile
     MfmaTiled64,    // 64x64x16 LDS double-buffered fp32 MFMA tile

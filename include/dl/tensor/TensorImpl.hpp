@@ -12,6 +12,7 @@
 #include <dl/core/DType.hpp>
 #include <dl/core/Device.hpp>
 #include <dl/core/Shape.hpp>
+#include <dl/tensor/StreamUseList.hpp>
 
 namespace dl {
 
@@ -71,7 +72,7 @@ public:
 private:
     void* data_ = nullptr;
     void* stream_ = nullptr;
-    mutable std::vector<void*> uses_;
+    mutable detail::StreamUseList uses_;
     Shape shape_;
     DType dtype_ = DType::Float32;
     Device device_;

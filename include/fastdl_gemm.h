@@ -313,6 +313,14 @@ int fdl_mlp2_graph_launch(fdl_mlp2_graph* graph, void* stream);
 int fdl_mlp2_graph_destroy(fdl_mlp2_graph* graph);
 
 /*
+ * Sets `bytes` bytes at `data` to zero, with a kernel on `stream` (null: the
+ * null stream).  Replaces the cudaMemset of TensorImpl::zero_
+ * (src/tensor/TensorImpl.cpp:143-154); a kernel rather than a memset, so that
+ * dl:: work captured into a graph replays correctly.
+ */
+int fdl_zero_fill(void* data, int64_t bytes, void* stream);
+
+/*
  * Fill with uniform values in (low, high] or normal values, from a
  * counter-based Philox4x32-10 stream keyed by seed (element i uses counter i).
  * Replaces the cuRAND fills of dl::kernels::uniform_float32 / normal_float32

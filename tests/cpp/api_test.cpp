@@ -5,6 +5,8 @@
 #include <dl/dl.hpp>
 #include <dl/kernels/kernels.hpp>
 
+#include <hip/hip_runtime_api.h>
+
 #include <cmath>
 #include <cstdint>
 #include <functional>
@@ -149,7 +151,10 @@ int main() {
         auto ta = dl::Tensor::from_host<float>(a, dl::Shape({m, k}), kDev);
         auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
         if (!close(dl::ops::matmul(ta, tb).to_host<float>(), want, 1e-5f)) return false;
-        for (auto algo : {dl::kernels::GemmAlgo::Auto, dl::kernels::GemmAlgo::MfmaTiled128,
+        // The reference's four names (gemm_benchmark.cu:87-99 runs each) and this build's.
+        for (auto algo : {dl::kernels::GemmAlgo::Naive, dl::kernels::GemmAlgo::Tiled,
+                          dl::kernels::GemmAlgo::Register, dl::kernels::GemmAlgo::Cublas,
+                          dl::kernels::GemmAlgo::Auto, dl::kernels::GemmAlgo::MfmaTiled128,
                           dl::kernels::GemmAlgo::MfmaTiled64, dl::kernels::GemmAlgo::MfmaSplitK}) {
             dl::Tensor tc(dl::Shape({m, n}), dl::DType::Float32, kDev);
             dl::kernels::gemm(static_cast<const float*>(ta.data()),
@@ -380,6 +385,50 @@ int main() {
         bool zeros = true;
         for (float v : zeroed) zeros = zeros && v == 0.0f;
         return ok && mm == ref_mm && lin == ref_lin && copied == ref_mm && zeros;
+    });
+
+    // Tensor::zeros inside a captured graph: zero_ is a kernel, not a memset
+    // node, so every replay zeroes the bias again (the bias and C are dirtied
+    // with NaN between replays by eager work on the same stream).
+    run("zeros_captured_in_a_graph_replays", [] {
+        const int m = 64, n = 48, k = 32;
+        const auto a = randv(static_cast<std::size_t>(m) * k, 41);
+        const auto b = randv(static_cast<std::size_t>(k) * n, 42);
+        const auto want = host_gemm(a, b, m, n, k);
+        dl::Stream s(kDev);
+        dl::StreamGuard guard(s);
+        const hipStream_t hs = static_cast<hipStream_t>(s.handle());
+        auto ta = dl::Tensor::from_host<float>(a, dl::Shape({m, k}), kDev);
+        auto tb = dl::Tensor::from_host<float>(b, dl::Shape({k, n}), kDev);
+        dl::Tensor c(dl::Shape({m, n}), dl::DType::Float32, kDev);
+        // a cached block of the bias's size on this stream: the capture allocates nothing
+        { dl::Tensor warm = dl::Tensor::zeros(dl::Shape({n}), dl::DType::Float32, kDev); }
+        s.synchronize();
+        dl::Tensor bias;
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        bool ok = hipStreamBeginCapture(hs, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        bias = dl::Tensor::zeros(dl::Shape({n}), dl::DType::Float32, kDev);
+        dl::kernels::gemm_ex(dl::kernels::Transpose::No, dl::kernels::Transpose::No, m, n, k,
+                             static_cast<const float*>(ta.data()), k, 0,
+                             static_cast<const float*>(tb.data()), n, 0,
+                             static_cast<float*>(c.data()), n, 0, 1,
+                             static_cast<const float*>(bias.data()), nullptr,
+                             dl::kernels::Epilogue::Bias, dl::kernels::GemmAlgo::Auto, hs);
+        ok = hipStreamEndCapture(hs, &graph) == hipSuccess && ok;
+        ok = ok && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+        const std::vector<float> nan_bias(n, std::nanf("")), nan_c(m * n, std::nanf(""));
+        for (int rep = 0; rep < 4 && ok; ++rep) {
+            bias.copy_from_host(nan_bias.data(), nan_bias.size() * sizeof(float));
+            c.copy_from_host(nan_c.data(), nan_c.size() * sizeof(float));
+            ok = hipGraphLaunch(exec, hs) == hipSuccess && hipStreamSynchronize(hs) == hipSuccess;
+            ok = ok && close(c.to_host<float>(), want, 1e-5f);
+            std::vector<float> zeros = bias.to_host<float>();
+            for (float v : zeros) ok = ok && v == 0.0f;
+        }
+        if (exec) ok = hipGraphExecDestroy(exec) == hipSuccess && ok;
+        if (graph) ok = hipGraphDestroy(graph) == hipSuccess && ok;
+        return ok;
     });
 
     run("mlp2_graph_replays_match_eager_steps_on_a_stream", [] {

@@ -33,6 +33,55 @@ def test_public_headers_are_plain_cxx(header, tmp_path):
     subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", INCLUDE, str(src)], check=True)
 
 
+REFERENCE_ALGO_NAMES = """
+#include <dl/kernels/gemm.hpp>
+#include <cstdio>
+#include <cstring>
+#include <initializer_list>
+
+// The reference's own spellings: src/ops/Matmul.cpp:42 passes GemmAlgo::Cublas to
+// gemm(), tests/benchmarks/gemm/gemm_benchmark.cu:87-99 runs each of the four.  Never
+// called here (no GPU); it only has to compile and link.
+void reference_calls(const float* a, const float* b, float* c, int m, int n, int k) {
+    dl::kernels::gemm(a, b, c, m, n, k, dl::kernels::GemmAlgo::Cublas);
+    for (auto algo : {dl::kernels::GemmAlgo::Naive, dl::kernels::GemmAlgo::Tiled,
+                      dl::kernels::GemmAlgo::Register, dl::kernels::GemmAlgo::Cublas}) {
+        dl::kernels::gemm(a, b, c, m, n, k, algo);
+    }
+}
+
+int main() {
+    // to_string as the reference's gemm.cu:183-195 spells it
+    const struct { dl::kernels::GemmAlgo algo; const char* name; } names[] = {
+        {dl::kernels::GemmAlgo::Naive, "naive"}, {dl::kernels::GemmAlgo::Tiled, "tiled"},
+        {dl::kernels::GemmAlgo::Register, "register"}, {dl::kernels::GemmAlgo::Cublas, "cublas"}};
+    for (const auto& e : names) {
+        if (std::strcmp(dl::kernels::to_string(e.algo), e.name) != 0) {
+            std::printf("to_string mismatch: %s\\n", e.name);
+            return 1;
+        }
+    }
+    std::printf("reference algo names ok\\n");
+    return reference_calls == nullptr;
+}
+"""
+
+
+def test_reference_gemm_algo_names_compile_and_print(tmp_path):
+    """A caller written against the reference's GemmAlgo (Naive, Tiled, Register, Cublas)
+    compiles and links unchanged, and to_string gives the reference's names."""
+    assert os.path.exists(LIB), "libfastdl.so not built"
+    src = tmp_path / "algo_names.cpp"
+    src.write_text(REFERENCE_ALGO_NAMES)
+    exe = tmp_path / "algo_names"
+    pkg = os.path.dirname(LIB)
+    subprocess.run(["g++", "-std=c++17", "-I", INCLUDE, str(src), "-o", str(exe), "-L", pkg,
+                    "-lfastdl", "-lfastdl_gemm", f"-Wl,-rpath,{pkg}"], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "reference algo names ok" in out.stdout
+
+
 def test_library_exports_api_symbols():
     assert os.path.exists(LIB), "libfastdl.so not built"
     out = subprocess.run(["nm", "-DC", "--defined-only", LIB], capture_output=True, text=True,

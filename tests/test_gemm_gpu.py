@@ -309,3 +309,40 @@ def test_splitk16_lds_staged(device, M, N, K, batch, epi):
     ci = gpu_sgemm(0, 0, Ai, Bi, M, N, K, batch=batch, kernel=capi.KERNEL_SPLITK16)
     exact = np.einsum("bmk,bkn->bmn", Ai.astype(np.int64), Bi.astype(np.int64))
     assert np.array_equal(ci, exact.astype(np.float32))
+
+
+@pytest.mark.parametrize("wide", ["lda", "ldb"])
+def test_splitk16_lds_form_wide_pitch_takes_register_form(device, wide):
+    """The LDS-staged split-K16 form addresses its copies with 32-bit offsets, so it takes
+    lda < 2^24 and ldb < 2^22; past either, the same problem runs the register form, which
+    gives the LDS form's bits.  The wide operand is a strided view of one large
+    allocation (2 GB for A, 13 GB for B), only its used elements written."""
+    import torch
+
+    M, N, K = 32, 16, 800
+    g = rng(4243 if wide == "lda" else 4244)
+    A, B = operands(g, 0, 0, M, N, K, 1)
+    bias = (g.standard_normal(N) * 0.1).astype(np.float32)
+    say(f"splitk16 with {wide} past the LDS form's offsets, M={M} N={N} K={K}")
+    c_lds = gpu_sgemm(0, 0, A, B, M, N, K, bias=bias, epilogue=capi.EPILOGUE_BIAS_RELU,
+                      kernel=capi.KERNEL_SPLITK16)
+    lda, ldb = K, N
+    if wide == "lda":
+        lda = 1 << 24
+        big = torch.empty((M - 1) * lda + K, dtype=torch.float32, device="cuda")
+        torch.as_strided(big, (M, K), (lda, 1)).copy_(torch.from_numpy(A[0]).cuda())
+        dA, dB = big, torch.from_numpy(B[0]).cuda()
+    else:
+        ldb = 1 << 22
+        big = torch.empty((K - 1) * ldb + N, dtype=torch.float32, device="cuda")
+        torch.as_strided(big, (K, N), (ldb, 1)).copy_(torch.from_numpy(B[0]).cuda())
+        dA, dB = torch.from_numpy(A[0]).cuda(), big
+    dbias = torch.from_numpy(bias).cuda()
+    dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    capi.sgemm_ex_select(0, 0, M, N, K, dA.data_ptr(), lda, 0, dB.data_ptr(), ldb, 0,
+                         dC.data_ptr(), N, 0, 1, dbias.data_ptr(), None,
+                         capi.EPILOGUE_BIAS_RELU, capi.KERNEL_SPLITK16, stream())
+    c_wide = host(dC).reshape(1, M, N)
+    del big
+    check_gemm(c_wide, 0, 0, A, B, M, N, K, bias=bias, epilogue=capi.EPILOGUE_BIAS_RELU)
+    assert np.array_equal(c_wide, c_lds)

@@ -66,7 +66,9 @@ def test_noalloc_without_scratch_and_beyond_it(device):
                           _gemm("plain", M, N, K, A, B, bias, 0))
     # one that needs more than the scratch holds is refused before any launch
     assert capi.workspace_size(0, 0, 8, 43776, 4096) > SCRATCH_BYTES
-    status = capi.raw_call("fdl_sgemm_ex_noalloc", 0, 0, 8, 43776, 4096, 1 << 20, 4096, 0,
-                           1 << 20, 43776, 0, 1 << 20, 43776, 0, 1, None, None, 0, None)
+    # null operands: the scratch-size refusal comes first, and were that check
+    # ever to regress, the null-pointer check still refuses before any launch
+    status = capi.raw_call("fdl_sgemm_ex_noalloc", 0, 0, 8, 43776, 4096, None, 4096, 0,
+                           None, 43776, 0, None, 43776, 0, 1, None, None, 0, None)
     assert status == -1
     assert "bytes of scratch" in capi.last_error()
