@@ -88,7 +88,7 @@ def build_gemm_library() -> str:
         list(ex.map(lambda so: _compile(so[0], so[1], True), zip(srcs, objs)))
     out = os.path.join(PKG, "libfastdl_gemm.so")
     tmp = out + ".tmp"
-    _run([HIPCC, *DEVICE_FLAGS, "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
     return out
 

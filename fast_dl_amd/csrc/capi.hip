@@ -413,9 +413,11 @@ int fdl_mlp2_train_step(const float* X, const int64_t* labels, int64_t batch,
         fin.lr = lr;
         fin.rows = B;
         fin.cols = Cc;
-        const fdl::GroupJob jobs[4] = {
+        fdl::GroupJob jobs[4] = {
             gemm_job(true, false, I, Hd, B, X, I, G1, Hd, dW1, fdl::EPI_SGD, nullptr, W1), db1_job,
             gemm_job(true, false, Hd, Cc, B, H, Hd, G2, Cc, dW2, fdl::EPI_SGD, nullptr, W2), fin};
+        // dW2 is Hd x Cc: with at most 16 classes, 16x16 output tiles
+        if (Cc <= 16) jobs[2].kind = fdl::GroupJob::kGemm16;
         return check_hip(fdl::launch_group(jobs, 4, hs), "mlp2_train_step backward failed");
     }
 

@@ -72,9 +72,11 @@ bool dma_supported(GemmKernel kernel, const GemmParams& p, bool transA, bool tra
 // partial records (xent_finalize_body), or the head's loss, db2 and b2 step
 // from its stored logits and G2 (head_finalize_body).
 struct GroupJob {
-    enum Kind { kGemm, kColsumSgd, kSgd, kXentFinalize, kHeadFinalize };
+    // kGemm16: the same GEMM on 16x16 output tiles (v_mfma_f32_16x16x4_f32), for
+    // outputs at most 16 wide, where a 32x32 tile would waste most of its work.
+    enum Kind { kGemm, kColsumSgd, kSgd, kXentFinalize, kHeadFinalize, kGemm16 };
     Kind kind = kGemm;
-    GemmParams p{};              // kGemm
+    GemmParams p{};              // kGemm, kGemm16
     bool ta = false, tb = false;
     const float* x = nullptr;    // kColsumSgd: rows x cols input; kSgd: gradient;
                                  // kXentFinalize: the partial records;
@@ -94,8 +96,8 @@ struct GroupJob {
 // of the grid.  Supported sequences are the ones the MLP step uses:
 // (NT GEMM, TN GEMM), (NT GEMM, column sum), (TN GEMM, SGD),
 // (NT GEMM, column sum, TN GEMM, finalize), (column sum, TN GEMM,
-// finalize) and (TN GEMM, column sum, TN GEMM, head finalize); others return
-// hipErrorInvalidValue.
+// finalize) and (TN GEMM, column sum, TN GEMM, head finalize), the second TN
+// GEMM of the last either kind; others return hipErrorInvalidValue.
 hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream);
 inline hipError_t launch_group2(const GroupJob& j0, const GroupJob& j1, hipStream_t stream) {
     const GroupJob jobs[2] = {j0, j1};

@@ -1610,22 +1610,25 @@ __device__ __forceinline__ void splitk16_load_group(const float* __restrict__ A,
     splitk_load_group<TA, TB, VA, VB>(A, B, p, row, col, kb, kend, tail, a, b);
 }
 
+// The body takes its block index and the number of blocks that share the
+// tile mapping explicitly, so a grouped launch can run it on a sub-range of
+// its grid (sgemm_group_kernel), as splitk32_body does.
 template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
-__global__ void __launch_bounds__(KW * 64)
-sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
+__device__ __forceinline__ void splitk16_body(const GemmParams& p, int tiles_m, int tiles_n,
+                                              int kchunk, int bid, int nblocks, int64_t bz) {
     __shared__ float red[KW][4][kWave];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    // wave-uniform, so the K-range tests are scalar branches (see splitk32_body)
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int i = lane & 15;
     const int q = lane >> 4;
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(bid, nblocks, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * 16;
     const int n0 = tn * 16;
-    const int64_t bz = blockIdx.y;
     const float* __restrict__ A = p.A + bz * p.strideA;
     const float* __restrict__ B = p.B + bz * p.strideB;
 
@@ -1707,6 +1710,13 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
             store_epilogue_pre(v, p, C, upd, (int64_t)gi * p.ldc + gj, pre[u]);
         }
     }
+}
+
+template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(KW * 64)
+sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
+    splitk16_body<KW, ITS, TA, TB, VA, VB>(p, tiles_m, tiles_n, kchunk, blockIdx.x, gridDim.x,
+                                           blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -2304,6 +2314,16 @@ struct JobGemm {
     }
 };
 
+// A kGemm16 job: four waves of 64 k each, all of a wave's k in flight.
+constexpr int kGroupITS16 = 4;
+template <bool TA, bool TB, bool VA, bool VB>
+struct JobGemm16 {
+    static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
+        splitk16_body<kGroupKW, kGroupITS16, TA, TB, VA, VB>(a.p, a.tiles_m, a.tiles_n,
+                                                             a.kchunk, bid, a.blocks, 0);
+    }
+};
+
 struct JobColsumSgd {
     static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
         colsum_body(a.x, a.out, a.param, a.lr, a.rows, a.cols, bid);
@@ -2786,6 +2806,15 @@ GroupDev group_dev(const GroupJob& j) {
             d.blocks = d.tiles_m * d.tiles_n;
             break;
         }
+        case GroupJob::kGemm16: {
+            d.tiles_m = (j.p.M + 15) / 16;
+            d.tiles_n = (j.p.N + 15) / 16;
+            constexpr int kSuper = 16 * kGroupITS16;
+            int kchunk = (j.p.K + kGroupKW - 1) / kGroupKW;
+            d.kchunk = std::max(kSuper, (kchunk + kSuper - 1) / kSuper * kSuper);
+            d.blocks = d.tiles_m * d.tiles_n;
+            break;
+        }
         case GroupJob::kColsumSgd:
             d.blocks = (int)((j.cols + kColsumCols - 1) / kColsumCols);
             break;
@@ -2828,7 +2857,8 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
     GroupArgs a{};
     for (int i = 0; i < n; ++i) {
         const GroupJob& j = jobs[i];
-        if (j.kind == GroupJob::kGemm && (j.p.M <= 0 || j.p.N <= 0 || j.p.K <= 0)) {
+        if ((j.kind == GroupJob::kGemm || j.kind == GroupJob::kGemm16) &&
+            (j.p.M <= 0 || j.p.N <= 0 || j.p.K <= 0)) {
             return hipErrorInvalidValue;
         }
         if (j.kind == GroupJob::kHeadFinalize &&
@@ -2844,7 +2874,11 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
         return jobs[i].kind == GroupJob::kGemm && jobs[i].ta && !jobs[i].tb;
     };
     auto is = [&](int i, GroupJob::Kind k) { return jobs[i].kind == k; };
+    auto is_tn16 = [&](int i) {
+        return jobs[i].kind == GroupJob::kGemm16 && jobs[i].ta && !jobs[i].tb;
+    };
     using TN = JobGemm<true, false, false, false>;
+    using TN16 = JobGemm16<true, false, false, false>;
     if (n == 2) {
         if (is_nt(0) && is_tn(1)) return launch_nt_first<TN>(jobs[0], a, stream);
         if (is_nt(0) && is(1, GroupJob::kColsumSgd)) {
@@ -2863,6 +2897,10 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
         if (is_tn(0) && is(1, GroupJob::kColsumSgd) && is_tn(2) &&
             is(3, GroupJob::kHeadFinalize)) {
             return launch_group_of<TN, JobColsumSgd, TN, JobHeadFinalize>(a, stream);
+        }
+        if (is_tn(0) && is(1, GroupJob::kColsumSgd) && is_tn16(2) &&
+            is(3, GroupJob::kHeadFinalize)) {
+            return launch_group_of<TN, JobColsumSgd, TN16, JobHeadFinalize>(a, stream);
         }
     }
     return hipErrorInvalidValue;
