@@ -1826,12 +1826,17 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
         copy(std::integral_constant<int, 1>{});
         copy(std::integral_constant<int, 2>{});
         copy(std::integral_constant<int, 3>{});
-        // Group g's MFMAs start as soon as its two copies have landed: the
-        // compiler, which must wait for a direct-to-LDS copy before reading
-        // what it wrote, tells the four arrays apart and waits for
-        // vmcnt(2 (GR - 1 - g)) before group g's reads (checked in the ISA).
+        // Nothing may move between the copies and the waits below.
+        __builtin_amdgcn_sched_barrier(0);
+        // Group g's MFMAs start as soon as its two copies have landed.  Loads
+        // complete in order and the epilogue operand was loaded before the
+        // copies, so once at most 2 (GR - 1 - g) operations (the later
+        // groups' copies) are outstanding, group g's have landed; the wait is
+        // written here rather than left to the compiler, which places the
+        // same one only because it tells the four arrays apart.
         auto group = [&](auto gc) {
             constexpr int g = decltype(gc)::value;
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (GR - 1 - g)));
             const int k0 = kbeg + 16 * g;
             if (k0 >= p.K) return;
             const float* as = region(gc);

@@ -82,6 +82,30 @@ def test_reference_gemm_algo_names_compile_and_print(tmp_path):
     assert "reference algo names ok" in out.stdout
 
 
+REFERENCE_ROOT = "/root/reference"
+
+
+@pytest.mark.skipif(not os.path.isdir(REFERENCE_ROOT), reason="reference sources not mounted")
+def test_every_gemm_algo_the_reference_names_compiles(tmp_path):
+    """Every `GemmAlgo::X` spelled anywhere in the reference's sources (src/ops/Matmul.cpp:42,
+    tests/benchmarks/gemm/gemm_benchmark.cu:87-99, ...) names an enumerator of this build's
+    dl/kernels/gemm.hpp.  The files themselves include CUDA headers (cuda_runtime.h,
+    dl/core/CudaUtils.hpp), so they are scanned as text, not compiled."""
+    import re
+    names = set()
+    for path in glob.glob(os.path.join(REFERENCE_ROOT, "**", "*.*"), recursive=True):
+        if os.path.splitext(path)[1] not in (".cpp", ".cu", ".hpp", ".cuh", ".h"):
+            continue
+        with open(path, errors="replace") as f:
+            names.update(re.findall(r"GemmAlgo::(\w+)", f.read()))
+    assert {"Naive", "Tiled", "Register", "Cublas"} <= names, sorted(names)
+    src = tmp_path / "names.cpp"
+    body = "\n".join(f"    (void)dl::kernels::to_string(dl::kernels::GemmAlgo::{n});"
+                     for n in sorted(names))
+    src.write_text(f"#include <dl/kernels/gemm.hpp>\nvoid f() {{\n{body}\n}}\n")
+    subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", INCLUDE, str(src)], check=True)
+
+
 def test_library_exports_api_symbols():
     assert os.path.exists(LIB), "libfastdl.so not built"
     out = subprocess.run(["nm", "-DC", "--defined-only", LIB], capture_output=True, text=True,
