@@ -354,15 +354,24 @@ def mlp_rate(capi, torch, steps=200, warmup=20):
     warm_clock(step, torch.cuda.current_stream())
     ms = time_launches(step, steps, warmup, torch.cuda.current_stream())
     loss = float(buf["loss"].item())
-    # The same step captured once into a HIP graph and replayed.
-    handle = capi.mlp2_graph_create(*args)
-    try:
-        warm_clock(lambda: capi.mlp2_graph_launch(handle, stream), torch.cuda.current_stream())
-        gms = time_launches(lambda: capi.mlp2_graph_launch(handle, stream), steps, warmup,
-                            torch.cuda.current_stream())
-    finally:
-        capi.mlp2_graph_destroy(handle)
-    return 1000.0 / ms, ms, loss, 1000.0 / gms, gms
+    # The same step captured into a HIP graph and replayed: one step per
+    # graph, and GRAPH_STEPS consecutive steps per graph (one host launch for
+    # all of them; ms per step = ms per replay / GRAPH_STEPS).
+    graph_ms = {}
+    for per in (1, GRAPH_STEPS):
+        handle = capi.mlp2_graph_create_steps(per, *args)
+        try:
+            launch = lambda: capi.mlp2_graph_launch(handle, stream)  # noqa: E731
+            warm_clock(launch, torch.cuda.current_stream())
+            replays = max(steps // per, 20)
+            graph_ms[per] = time_launches(launch, replays, max(warmup // per, 2),
+                                          torch.cuda.current_stream()) / per
+        finally:
+            capi.mlp2_graph_destroy(handle)
+    return 1000.0 / ms, ms, loss, graph_ms
+
+
+GRAPH_STEPS = 64  # steps per graph in the multi-step replay figure
 
 
 IDX_COUNT, IDX_PIXELS, IDX_BATCH = 60000, 784, 256  # MNIST train set: 60000 records of 28x28
@@ -597,11 +606,13 @@ def sweep(capi, torch, path):
                 "per_batch_steps_per_s": ep["per_batch"]["steps_per_s"],
                 "whole_epoch_steps_per_s": ep["whole_epoch"]["steps_per_s"]})
     print(json.dumps(out[-1]), file=sys.stderr, flush=True)
-    sps, ms, _, gsps, gms = mlp_rate(capi, torch)
+    sps, ms, _, gms = mlp_rate(capi, torch)
     tsps, tms = torch_mlp_rate(torch)
     out.append({"config": "C2 MLP 784-256-10 b256 step", "ms": ms, "steps_per_s": sps,
-                "graph_ms": gms, "graph_steps_per_s": gsps, "torch_eager_ms": tms,
-                "torch_eager_steps_per_s": tsps})
+                "graph_ms": gms[1], "graph_steps_per_s": 1000.0 / gms[1],
+                f"graph{GRAPH_STEPS}_ms": gms[GRAPH_STEPS],
+                f"graph{GRAPH_STEPS}_steps_per_s": 1000.0 / gms[GRAPH_STEPS],
+                "torch_eager_ms": tms, "torch_eager_steps_per_s": tsps})
     print(json.dumps(out[-1]), file=sys.stderr, flush=True)
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
@@ -646,7 +657,7 @@ def main():
         if cfg == "mlp" and args.profile_vendor:
             _, pms = torch_mlp_rate(torch, steps=args.steps, warmup=args.warmup)
         elif cfg == "mlp":
-            _, pms, _, _, _ = mlp_rate(capi, torch, steps=args.steps, warmup=args.warmup)
+            _, pms, _, _ = mlp_rate(capi, torch, steps=args.steps, warmup=args.warmup)
         else:
             M, N, K, tb, batch, epi, rot = cfg
             if args.profile_vendor:
@@ -678,13 +689,18 @@ def main():
 
     mlp = None
     if not args.no_mlp:
-        sps, mlp_ms, loss, graph_sps, graph_ms = mlp_rate(capi, torch)
+        sps, mlp_ms, loss, graph_ms = mlp_rate(capi, torch)
         mlp = {"steps_per_s": sps, "ms_per_step": mlp_ms,
-               "graph_steps_per_s": graph_sps, "graph_ms_per_step": graph_ms,
+               "graph_steps_per_s": 1000.0 / graph_ms[1], "graph_ms_per_step": graph_ms[1],
+               f"graph{GRAPH_STEPS}_steps_per_s": 1000.0 / graph_ms[GRAPH_STEPS],
+               f"graph{GRAPH_STEPS}_ms_per_step": graph_ms[GRAPH_STEPS],
                "final_loss": loss,
                "config": "784-256-10, batch 256, lr 0.1, full step (forward, softmax-CE, "
                          "backward incl. dX, SGD): one fdl_mlp2_train_step call (3 launches) "
-                         "per step; graph = the same step replayed as a HIP graph"}
+                         "per step; graph = the same step replayed as a HIP graph; "
+                         f"graph{GRAPH_STEPS} = {GRAPH_STEPS} consecutive steps captured in "
+                         "one graph (fdl_mlp2_graph_create_steps), one replay per "
+                         f"{GRAPH_STEPS} steps"}
     idx = None
     if not args.no_mlp:
         idx = idx_data_rate(capi, torch)

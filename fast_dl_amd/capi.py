@@ -58,6 +58,9 @@ SIGNATURES = {
     "fdl_mlp2_graph_create": (_int, [ctypes.POINTER(_vp), _vp, _vp, _i64, _i64, _i64, _i64,
                                      _vp, _vp, _vp, _vp, _flt, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _vp, _vp]),
+    "fdl_mlp2_graph_create_steps": (_int, [ctypes.POINTER(_vp), _int, _vp, _vp, _i64, _i64,
+                                           _i64, _i64, _vp, _vp, _vp, _vp, _flt, _vp, _vp,
+                                           _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "fdl_mlp2_graph_launch": (_int, [_vp, _vp]),
     "fdl_mlp2_graph_destroy": (_int, [_vp]),
     "fdl_zero_fill": (_int, [_vp, _i64, _vp]),
@@ -139,6 +142,16 @@ def mlp2_graph_create(*args) -> int:
     status = lib.fdl_mlp2_graph_create(ctypes.byref(handle), *args)
     if status != 0:
         raise FdlError("fdl_mlp2_graph_create", status, lib.fdl_last_error().decode())
+    return handle.value
+
+
+def mlp2_graph_create_steps(steps: int, *args) -> int:
+    """Capture `steps` consecutive fdl_mlp2_train_step(*args) calls into one graph."""
+    handle = ctypes.c_void_p()
+    lib = load_library()
+    status = lib.fdl_mlp2_graph_create_steps(ctypes.byref(handle), steps, *args)
+    if status != 0:
+        raise FdlError("fdl_mlp2_graph_create_steps", status, lib.fdl_last_error().decode())
     return handle.value
 
 

@@ -517,13 +517,15 @@ struct fdl_mlp2_graph {
 
 extern "C" {
 
-int fdl_mlp2_graph_create(fdl_mlp2_graph** out, const float* X, const int64_t* labels,
-                          int64_t batch, int64_t in_features, int64_t hidden, int64_t classes,
-                          float* W1, float* b1, float* W2, float* b2, float lr, float* H,
-                          float* logits, float* G2, float* G1, float* dW1, float* db1,
-                          float* dW2, float* db2, float* dX, float* loss, void* stream) {
+int fdl_mlp2_graph_create_steps(fdl_mlp2_graph** out, int steps, const float* X,
+                                const int64_t* labels, int64_t batch, int64_t in_features,
+                                int64_t hidden, int64_t classes, float* W1, float* b1, float* W2,
+                                float* b2, float lr, float* H, float* logits, float* G2,
+                                float* G1, float* dW1, float* db1, float* dW2, float* db2,
+                                float* dX, float* loss, void* stream) {
     if (!out) return fail(FDL_ERROR_INVALID_VALUE, "mlp2_graph_create: null handle pointer");
     *out = nullptr;
+    if (steps < 1) return fail(FDL_ERROR_INVALID_VALUE, "mlp2_graph_create: steps must be >= 1");
     hipStream_t s = as_stream(stream);
     hipStream_t own = nullptr;
     if (s == nullptr) {
@@ -539,9 +541,11 @@ int fdl_mlp2_graph_create(fdl_mlp2_graph** out, const float* X, const int64_t* l
         cleanup();
         return check_hip(e, "mlp2_graph_create: begin capture");
     }
-    const int st = fdl_mlp2_train_step(X, labels, batch, in_features, hidden, classes, W1, b1,
-                                       W2, b2, lr, H, logits, G2, G1, dW1, db1, dW2, db2, dX,
-                                       loss, s);
+    int st = FDL_SUCCESS;
+    for (int i = 0; i < steps && st == FDL_SUCCESS; ++i) {
+        st = fdl_mlp2_train_step(X, labels, batch, in_features, hidden, classes, W1, b1, W2, b2,
+                                 lr, H, logits, G2, G1, dW1, db1, dW2, db2, dX, loss, s);
+    }
     hipGraph_t graph = nullptr;
     e = hipStreamEndCapture(s, &graph);
     if (st != FDL_SUCCESS || e != hipSuccess) {
@@ -561,6 +565,16 @@ int fdl_mlp2_graph_create(fdl_mlp2_graph** out, const float* X, const int64_t* l
     g->exec = exec;
     *out = g;
     return FDL_SUCCESS;
+}
+
+int fdl_mlp2_graph_create(fdl_mlp2_graph** out, const float* X, const int64_t* labels,
+                          int64_t batch, int64_t in_features, int64_t hidden, int64_t classes,
+                          float* W1, float* b1, float* W2, float* b2, float lr, float* H,
+                          float* logits, float* G2, float* G1, float* dW1, float* db1,
+                          float* dW2, float* db2, float* dX, float* loss, void* stream) {
+    return fdl_mlp2_graph_create_steps(out, 1, X, labels, batch, in_features, hidden, classes,
+                                       W1, b1, W2, b2, lr, H, logits, G2, G1, dW1, db1, dW2,
+                                       db2, dX, loss, stream);
 }
 
 int fdl_mlp2_graph_launch(fdl_mlp2_graph* g, void* stream) {

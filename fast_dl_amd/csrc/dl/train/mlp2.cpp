@@ -71,15 +71,19 @@ float Mlp2::step(const float* x, const int64_t* labels, float lr, bool sync_loss
     return loss_.to_host<float>()[0];
 }
 
-void Mlp2::capture(const Tensor& x, const Tensor& labels, float lr) {
+void Mlp2::capture(const Tensor& x, const Tensor& labels, float lr) { capture(x, labels, lr, 1); }
+
+void Mlp2::capture(const Tensor& x, const Tensor& labels, float lr, int steps) {
     check_batch(x, labels, "Mlp2::capture");
+    if (steps < 1) throw std::runtime_error("Mlp2::capture: steps must be at least 1");
     hip::check(hipSetDevice(x.device().index), "cudaSetDevice failed");
     fdl_mlp2_graph* g = nullptr;
-    hip::check_fdl(fdl_mlp2_graph_create(&g, fp(x), static_cast<const int64_t*>(labels.data()), batch_,
-                                         in_, hidden_, classes_, fp(w1_), fp(b1_), fp(w2_), fp(b2_),
-                                         lr, fp(h_), fp(logits_), fp(g2_), fp(g1_), fp(dw1_),
-                                         fp(db1_), fp(dw2_), fp(db2_), fp(dx_), fp(loss_),
-                                         current_stream()),
+    hip::check_fdl(fdl_mlp2_graph_create_steps(&g, steps, fp(x),
+                                               static_cast<const int64_t*>(labels.data()), batch_,
+                                               in_, hidden_, classes_, fp(w1_), fp(b1_), fp(w2_),
+                                               fp(b2_), lr, fp(h_), fp(logits_), fp(g2_), fp(g1_),
+                                               fp(dw1_), fp(db1_), fp(dw2_), fp(db2_), fp(dx_),
+                                               fp(loss_), current_stream()),
                    "Mlp2::capture failed");
     graph_ = std::shared_ptr<fdl_mlp2_graph>(g, [](fdl_mlp2_graph* p) { (void)fdl_mlp2_graph_destroy(p); });
     graph_x_ = x;

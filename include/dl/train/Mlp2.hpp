@@ -36,10 +36,13 @@ public:
     // replayed with one launch per step.  capture() records a step on x and
     // labels with learning rate lr (refill their buffers in place between
     // replays); nothing runs until replay().  Capturing again replaces the
-    // graph.  replay() runs one captured step on the current stream and
-    // returns the pre-update loss when sync_loss is true, else NaN; it throws
-    // if nothing was captured.
+    // graph.  replay() runs the captured steps on the current stream and
+    // returns the last step's pre-update loss when sync_loss is true, else
+    // NaN; it throws if nothing was captured.  With `steps` > 1 the graph
+    // holds that many consecutive steps on the same batch, so one replay
+    // costs one host launch for all of them.
     void capture(const Tensor& x, const Tensor& labels, float lr);
+    void capture(const Tensor& x, const Tensor& labels, float lr, int steps);
     float replay(bool sync_loss = true);
 
     Tensor& w1() { return w1_; }

@@ -309,6 +309,21 @@ int fdl_mlp2_graph_create(fdl_mlp2_graph** graph,
                           float* H, float* logits, float* G2, float* G1,
                           float* dW1, float* db1, float* dW2, float* db2,
                           float* dX, float* loss, void* stream);
+/*
+ * The same with `steps` (>= 1) consecutive training steps in the one graph,
+ * so that a replay runs them all for one host launch: each step reads the
+ * parameters the one before it updated, as the same number of
+ * fdl_mlp2_train_step calls would.  fdl_mlp2_graph_create is steps = 1.
+ * No reference counterpart, as above.
+ */
+int fdl_mlp2_graph_create_steps(fdl_mlp2_graph** graph, int steps,
+                                const float* X, const int64_t* labels,
+                                int64_t batch, int64_t in_features,
+                                int64_t hidden, int64_t classes,
+                                float* W1, float* b1, float* W2, float* b2, float lr,
+                                float* H, float* logits, float* G2, float* G1,
+                                float* dW1, float* db1, float* dW2, float* db2,
+                                float* dX, float* loss, void* stream);
 int fdl_mlp2_graph_launch(fdl_mlp2_graph* graph, void* stream);
 int fdl_mlp2_graph_destroy(fdl_mlp2_graph* graph);
 

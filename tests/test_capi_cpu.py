@@ -1,6 +1,7 @@
 """CPU-side checks of the C-ABI library: it loads, exports every symbol the
 public header declares, and rejects invalid arguments before touching a GPU
 (validation never calls into the HIP runtime)."""
+import ctypes
 import glob
 import os
 import re
@@ -80,6 +81,11 @@ def test_other_entry_points_validate():
                          1 << 20, 16, 0, 1, None, None, 0, capi.KERNEL_DMA256, None) == -2
     assert capi.raw_call("fdl_mlp2_train_step", *([None] * 2), 0, 1, 1, 1, *([None] * 4), 0.1,
                          *([None] * 11)) == -1
+    # a graph of no steps is refused before any capture
+    handle = ctypes.c_void_p()
+    assert capi.raw_call("fdl_mlp2_graph_create_steps", ctypes.byref(handle), 0, *([None] * 2),
+                         256, 784, 256, 10, *([None] * 4), 0.1, *([None] * 11)) == -1
+    assert "steps" in capi.last_error() and handle.value is None
 
 
 def test_kernel_choice():

@@ -124,6 +124,7 @@ def test_library_exports_api_symbols():
                 "dl::current_stream()", "dl::StreamGuard::StreamGuard(void*)",
                 "dl::Stream::Stream(dl::Device const&)",
                 "dl::train::Mlp2::capture(dl::Tensor const&, dl::Tensor const&, float)",
+                "dl::train::Mlp2::capture(dl::Tensor const&, dl::Tensor const&, float, int)",
                 "dl::train::Mlp2::replay(bool)",
                 "dl::data::DataLoader::DataLoader(std::__cxx11::basic_string<",
                 "dl::data::DataLoader::gather(dl::Tensor const&, long, long, dl::Tensor&, "

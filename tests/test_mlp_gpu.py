@@ -271,6 +271,39 @@ def test_mlp_graph_replays_match_eager(device):
         capi.mlp2_graph_destroy(handle)
 
 
+def test_mlp_multi_step_graph_matches_eager_steps(device):
+    # A graph of three consecutive steps, replayed twice, leaves every buffer
+    # as six eager steps do (each step reads what the previous one updated).
+    import torch
+
+    g = rng(78)
+    B, I, H, C = 256, 784, 256, 10
+    X = g.random((B, I)).astype(np.float32)
+    labels = g.integers(0, C, B).astype(np.int64)
+    W1 = g.uniform(-np.sqrt(6 / I), np.sqrt(6 / I), (I, H)).astype(np.float32)
+    W2 = g.uniform(-np.sqrt(6 / H), np.sqrt(6 / H), (H, C)).astype(np.float32)
+    b1 = np.zeros(H, np.float32)
+    b2 = np.zeros(C, np.float32)
+    te, eargs = _alloc_step(X, labels, W1, b1, W2, b2)
+    tg, gargs = _alloc_step(X, labels, W1, b1, W2, b2)
+    s = stream()
+    say("mlp2 graph create (3 steps)")
+    handle = capi.mlp2_graph_create_steps(3, *gargs, s)
+    try:
+        for rep in range(2):
+            say(f"mlp2 3-step graph replay {rep}")
+            for _ in range(3):
+                capi.mlp2_train_step(*eargs, s)
+            capi.mlp2_graph_launch(handle, s)
+            torch.cuda.synchronize()
+            junk = torch.randn(1000, device="cuda").sum().item()  # unrelated eager work
+            assert np.isfinite(junk)
+            for k in ("W1", "b1", "W2", "b2", "loss", "dX", "G1", "dW1", "db1", "dW2", "db2"):
+                assert torch.equal(te[k], tg[k]), f"replay {rep}: {k} differs"
+    finally:
+        capi.mlp2_graph_destroy(handle)
+
+
 def test_random_fills(device):
     import torch
 
