@@ -950,10 +950,16 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
         opa.issue(A, p.lda, t * BK, p.K, As + s * OpA::STAGE, tid);
         opb.issue(B, p.ldb, t * BK, p.K, Bs + s * OpB::STAGE, tid);
     };
+    // A K range of at most S tiles is copied whole up front, each tile into
+    // its own stage (the pipelined loop issues only S - 1 ahead and the last
+    // tile after the first has landed).  The cross-tile pipeline keeps its
+    // own schedule.
+    const bool all_ahead = !Cfg::XPIPE && ktiles <= S;
 #pragma unroll
     for (int s = 0; s < S - 1; ++s) {
         if (s < ktiles) issue_tile(s, s);
     }
+    if (all_ahead && ktiles == S) issue_tile(S - 1, S - 1);
 
     float a[2][4][FM];
     float b[2][4][FN];
@@ -1314,6 +1320,64 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
             ktile_last(t, cur);
             cur = next_stage(cur);
         }
+    } else if (NG % 2 == 0 && all_ahead && tail_tile < 0) {
+        // Every tile is in its own stage, so the only wait before reading tile
+        // t+1 is for its copies (each wave's own, then the barrier for the
+        // others').  That wait and the first fragment reads of tile t+1 come
+        // before the MFMAs of tile t's last group, so the reads' latency and
+        // the barrier overlap those MFMAs instead of stalling the next tile.
+        // Whole K-tiles only, and the tile count a template constant: with
+        // straight-line code and no masking branch, each group's MFMAs wait
+        // for that group's fragment reads alone (at a loop's back edge or a
+        // branch the waits fall back to every outstanding read).
+        auto run = [&](auto kt) __attribute__((always_inline)) {
+            constexpr int KT = decltype(kt)::value;
+            auto land = [&](auto tc) __attribute__((always_inline)) {
+                constexpr int later = KT - 1 - decltype(tc)::value;  // in flight after it
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(later * PER_TILE));
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            };
+            auto read_tile_group = [&](int t, int g, int slot) __attribute__((always_inline)) {
+                read_group(As + t * OpA::STAGE, Bs + t * OpB::STAGE, g, slot, t,
+                           std::false_type{});
+            };
+            auto tile = [&](auto tc) __attribute__((always_inline)) {
+                constexpr int t = decltype(tc)::value;
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    // NG is even, so group 0 of tile t+1 takes slot (g + 1) & 1 = 0
+                    if (g + 1 < NG) {
+                        read_tile_group(t, g + 1, (g + 1) & 1);
+                    } else if constexpr (t + 1 < KT) {
+                        land(std::integral_constant<int, t + 1>{});
+                        read_tile_group(t + 1, 0, 0);
+                    }
+                    if (!Cfg::ILV) __builtin_amdgcn_sched_barrier(0);
+                    mfma_group(g & 1);
+                    if (g + 1 < NG) interleave_hint();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            land(std::integral_constant<int, 0>{});
+            read_tile_group(0, 0, 0);
+            tile(std::integral_constant<int, 0>{});
+            if constexpr (KT > 1) tile(std::integral_constant<int, 1>{});
+            if constexpr (KT > 2) tile(std::integral_constant<int, 2>{});
+            if constexpr (KT > 3) tile(std::integral_constant<int, 3>{});
+        };
+        static_assert(S <= 4, "tile counts 1 to 4 below");
+        if (ktiles == 1) {
+            run(std::integral_constant<int, 1>{});
+        } else if (ktiles == 2) {
+            run(std::integral_constant<int, 2>{});
+        } else if (S >= 3 && ktiles == 3) {
+            run(std::integral_constant<int, (S >= 3 ? 3 : 1)>{});
+        } else if (S >= 4) {
+            run(std::integral_constant<int, (S >= 4 ? 4 : 1)>{});
+        }
     } else {
         int stage = 0;
         for (int t = 0; t < ktiles; ++t) {
@@ -1329,7 +1393,7 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (t + S - 1 < ktiles) {
+            if (!all_ahead && t + S - 1 < ktiles) {
                 issue_tile(t + S - 1, stage == 0 ? S - 1 : stage - 1);  // (t + S - 1) % S
             }
             const float* as = As + stage * OpA::STAGE;
