@@ -1900,6 +1900,9 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
         // same one only because it tells the four arrays apart.
         auto group = [&](auto gc) {
             constexpr int g = decltype(gc)::value;
+            // (the barrier keeps the scheduler from lifting this wait above
+            // the previous group's MFMAs)
+            __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (GR - 1 - g)));
             const int k0 = kbeg + 16 * g;
             if (k0 >= p.K) return;
@@ -2071,6 +2074,7 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
 // repeat bit for bit.
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 4;
+constexpr int kPartMaxRows = 512;  // slice rows whose A values the partial pass stages in LDS
 constexpr int64_t kSplitMinElems = int64_t(1) << 23;   // 32 MB of B
 
 template <int MR, bool TA, int UNR>
@@ -2078,6 +2082,8 @@ __global__ void __launch_bounds__(kSplitWaves * kWave)
 sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part) {
     constexpr int NW = kSplitWaves;
     __shared__ float red[NW][MR][kSplitBand];
+    // A's slice for MR > 2 (see below); MR <= 2 keeps A in scalar loads
+    __shared__ __attribute__((aligned(16))) float as_lds[MR > 2 ? kPartMaxRows * MR : 1];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     // wave-uniform, so A's loads below have wave-uniform addresses
@@ -2147,6 +2153,58 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
         }
         if (it < groups) {
             fma_rows(b0, a0);
+            k += NW * UNR;
+        }
+    } else if (rows <= kPartMaxRows) {
+        // Larger M: A's slice (rows x MR floats) is staged in LDS once, so
+        // the loop's only global loads are B's and its rows are software-
+        // pipelined as above (with A in scalar loads the loop waited for all
+        // of a group's MR * UNR A values, one cache round trip per group, and
+        // a second set of them did not fit).  Same k order and sums, so the
+        // same bits.
+        const int nrows = k1 - k0;
+        for (int e = tid; e < nrows * MR; e += NW * kWave) {
+            int kk, m;
+            if (TA) {
+                kk = e / MR;  // A is K x M: consecutive e along m
+                m = e - kk * MR;
+            } else {
+                m = e / nrows;  // A is M x K: consecutive e along k
+                kk = e - m * nrows;
+            }
+            as_lds[kk * MR + m] = a_at(m, k0 + kk);
+        }
+        __syncthreads();
+        auto load_b = [&](int kk, floatx4 (&b)[UNR]) {
+#pragma unroll
+            for (int u = 0; u < UNR; ++u)
+                b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * p.ldb + n0);
+        };
+        auto fma_lds = [&](int kk, const floatx4 (&b)[UNR]) {
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                const float* ar = as_lds + (kk + NW * u - k0) * MR;
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(ar[m], b[u][c], acc[m][c]);
+            }
+        };
+        const int span = k1 - k - NW * (UNR - 1);
+        const int groups = span > 0 ? (span + NW * UNR - 1) / (NW * UNR) : 0;
+        floatx4 b0[UNR], b1[UNR];
+        if (groups > 0) load_b(k, b0);
+        int it = 0;
+        for (; it + 2 <= groups; it += 2) {
+            load_b(k + NW * UNR, b1);
+            fma_lds(k, b0);
+            k += NW * UNR;
+            if (it + 2 < groups) load_b(k + NW * UNR, b0);
+            fma_lds(k, b1);
+            k += NW * UNR;
+        }
+        if (it < groups) {
+            fma_lds(k, b0);
             k += NW * UNR;
         }
     } else {
