@@ -113,20 +113,20 @@ __device__ __forceinline__ void xent_finalize_body(const float* __restrict__ par
     }
 }
 
-// The MLP head's reductions from its stored outputs (one block of 256
-// threads, classes <= kColsumCols): db = column sums of G with the bias step
-// bparam -= lr * db (the sums and their order exactly as colsum_body's), and
-// the loss, each row's share (logf(sum_c expf(z_c - max)) + max - z_label) /
-// rows computed from its stored logits z as the head computes it (classes in
-// order; rows with a label outside [0, classes) add nothing).  A thread takes
-// rows t, t + 256, ... for the loss; the shares are summed in row order per
-// thread, then over each wave by a fixed exchange tree and over the waves in
-// order.  Every load of the first 256 rows (the row's logits and label, the
-// bias, and 32 rows of G per thread for the column sums, at clamped
-// addresses) is issued before any is used, so the loss is computed while the
-// column sums' rows are still arriving.
+// The MLP head's reductions from its stored outputs, split over two blocks
+// of 256 threads (classes <= kColsumCols) so that their loads proceed side by
+// side.  Block `which` = 0: the loss, each row's share
+// (logf(sum_c expf(z_c - max)) + max - z_label) / rows computed from its
+// stored logits z as the head computes it (classes in order; rows with a
+// label outside [0, classes) add nothing); a thread takes rows t, t + 256,
+// ..., summed in row order, then over each wave by a fixed exchange tree and
+// over the waves in order.  Block 1: db = column sums of G with the bias step
+// bparam -= lr * db, the sums and their order exactly as colsum_body's.  Each
+// block issues all its loads of the first 256 rows (the rows' logits and
+// labels; the bias and 32 rows of G per thread) at clamped addresses before
+// it uses any.
 template <int CM>
-__device__ __forceinline__ void head_finalize_body(const float* __restrict__ logits,
+__device__ __forceinline__ void head_finalize_body(int which, const float* __restrict__ logits,
                                                    const float* __restrict__ g,
                                                    const int64_t* __restrict__ labels,
                                                    int64_t rows, int64_t classes,
@@ -139,25 +139,15 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
     __shared__ float wpart[kColsumThreads / 64];
     constexpr int kFirst = 32;  // column-sum rows per thread issued up front
     const int t = threadIdx.x;
-    const int cl = t % kColsumCols;
-    const int grp = t / kColsumCols;
-    const int64_t cc = cl < classes ? cl : classes - 1;
-    const int64_t r0 = t < rows ? t : rows - 1;
-    float z[CM];
+    if (which == 0) {
+        if (!loss) return;
+        const int64_t r0 = t < rows ? t : rows - 1;
+        float z[CM];
 #pragma unroll
-    for (int c = 0; c < CM; ++c) z[c] = logits[r0 * classes + (c < classes ? c : classes - 1)];
-    const int64_t label0 = labels[r0];
-    const float pv = bparam ? bparam[cc] : 0.0f;
-    float gv[kFirst];
-#pragma unroll
-    for (int u = 0; u < kFirst; ++u) {
-        const int64_t r = grp + (int64_t)u * kColsumGroups;
-        gv[u] = g[(r < rows ? r : rows - 1) * classes + cc];
-    }
-
-    float s = 0.0f;
-    if (loss) {
+        for (int c = 0; c < CM; ++c) z[c] = logits[r0 * classes + (c < classes ? c : classes - 1)];
+        const int64_t label0 = labels[r0];
         const float inv_b = 1.0f / (float)rows;
+        float s = 0.0f;
         for (int64_t r = t; r < rows; r += kColsumThreads) {
             int64_t label = label0;
             if (r != t) {  // rows past the first 256: load them here
@@ -185,9 +175,28 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if ((t & 63) == 0) wpart[t >> 6] = s;
+        __syncthreads();
+        if (t == 0) {
+            float l = wpart[0];
+#pragma unroll
+            for (int i = 1; i < kColsumThreads / 64; ++i) l += wpart[i];
+            loss[0] = l;
+        }
+        return;
     }
 
     // Column sums, rows grp, grp + 8, ... in order (colsum_body's order).
+    const int cl = t % kColsumCols;
+    const int grp = t / kColsumCols;
+    const int64_t cc = cl < classes ? cl : classes - 1;
+    const float pv = bparam ? bparam[cc] : 0.0f;
+    float gv[kFirst];
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u) {
+        const int64_t r = grp + (int64_t)u * kColsumGroups;
+        gv[u] = g[(r < rows ? r : rows - 1) * classes + cc];
+    }
     float cs = 0.0f;
 #pragma unroll
     for (int u = 0; u < kFirst; ++u) {
@@ -210,7 +219,6 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
     }
     for (; r < rows; r += kColsumGroups) cs += g[r * classes + cc];
     part[grp][cl] = cs;
-    if ((t & 63) == 0) wpart[t >> 6] = s;
     __syncthreads();
     if (grp == 0 && cl < classes) {
         float tsum = part[0][cl];
@@ -221,12 +229,6 @@ __device__ __forceinline__ void head_finalize_body(const float* __restrict__ log
         wait_vmem_idle();
         db[cl] = tsum;
         if (bparam) bparam[cl] = np;
-    }
-    if (t == 0 && loss) {
-        float l = wpart[0];
-#pragma unroll
-        for (int i = 1; i < kColsumThreads / 64; ++i) l += wpart[i];
-        loss[0] = l;
     }
 }
 

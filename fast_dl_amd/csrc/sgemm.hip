@@ -2469,14 +2469,15 @@ struct JobXentFinalize {
     }
 };
 
+// Two blocks: block 0 the loss, block 1 db and the bias step.
 struct JobHeadFinalize {
-    static __device__ __forceinline__ void run(const GroupDev& a, int) {
+    static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
         if (a.cols <= 16) {
-            head_finalize_body<16>(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out, a.param,
-                                   a.lr);
+            head_finalize_body<16>(bid, a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out,
+                                   a.param, a.lr);
         } else {
-            head_finalize_body<kColsumCols>(a.x, a.x2, a.labels, a.rows, a.cols, a.out2, a.out,
-                                            a.param, a.lr);
+            head_finalize_body<kColsumCols>(bid, a.x, a.x2, a.labels, a.rows, a.cols, a.out2,
+                                            a.out, a.param, a.lr);
         }
     }
 };
@@ -2949,8 +2950,10 @@ GroupDev group_dev(const GroupJob& j) {
             d.blocks = (int)std::min<int64_t>((j.rows + 4 * 256 - 1) / (4 * 256), 1024);
             break;
         case GroupJob::kXentFinalize:
-        case GroupJob::kHeadFinalize:
             d.blocks = 1;
+            break;
+        case GroupJob::kHeadFinalize:
+            d.blocks = 2;
             break;
     }
     return d;
