@@ -56,6 +56,22 @@ def test_dma_integer_inputs_bit_exact(device, fam, bk, ta, tb):
     assert np.array_equal(c, (opA @ opB).astype(np.float32))
 
 
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+@pytest.mark.parametrize("K", [16, 32, 48, 64, 4, 28, 60])
+def test_dma64s_short_k_bit_exact(device, ta, tb, K):
+    # K <= 64 in whole 16-deep K-tiles (1 to 4) runs the straight-line form
+    # with every K-tile copied up front; a partial last tile (4, 28, 60) runs
+    # the loop.  Small integers: every product and partial sum is exact.
+    M, N = 200, 136
+    A, B = operands(_rng(19, K, ta, tb), ta, tb, M, N, K, 2, dist="int")
+    say(f"dma64s short K={K} ta={ta} tb={tb}")
+    c = gpu_sgemm(ta, tb, A, B, M, N, K, batch=2, kernel=capi.KERNEL_DMA64S)
+    for z in range(2):
+        opA = (A[z].T if ta else A[z]).astype(np.int64)
+        opB = (B[z].T if tb else B[z]).astype(np.int64)
+        assert np.array_equal(c[z], (opA @ opB).astype(np.float32)), f"batch {z}"
+
+
 @pytest.mark.parametrize("fam,bk", DMAS)
 @pytest.mark.parametrize("epi", [capi.EPILOGUE_BIAS, capi.EPILOGUE_BIAS_RELU,
                                  capi.EPILOGUE_RELU, capi.EPILOGUE_RELU_GRAD])
