@@ -496,10 +496,11 @@ __device__ __forceinline__ float row16_sum(float x) {
 //     hidden range; the other parts' sums reach part 0's wave through LDS
 //     and are added in part order.
 // W2 is staged in LDS as rows of CM floats (stride CM + 4), zero past
-// `hidden` rows and `classes` columns.  Every global load is issued before
-// the first wait (the W1 fragments last: loads complete in order, so the
-// staging waits only for the loads before them), at addresses clamped into
-// the arrays, and values outside the problem are zeroed where they are used.
+// `hidden` rows and `classes` columns.  The head's global loads are all
+// issued before its first wait, and dX's W1 fragments right after the
+// staging barrier (loads complete in order, so the head's waits never count
+// them), all at addresses clamped into the arrays; values outside the
+// problem are zeroed where they are used.
 // Needs hidden <= 256, hidden % 4 == 0, classes <= 16 * CT, and H and W1
 // 16-byte aligned (the host checks).
 constexpr int kHdxThreads = kHdxRows * 32;
@@ -568,16 +569,11 @@ mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
         for (int r = 0; r < 4; ++r)
             hm[tt][r] = H[(int64_t)min(r0 + 4 * q + r, batch - 1) * hidden +
                           min(16 * (2 * w + tt) + i16, hidden - 1)];
-    // dX operand b: W1[col][k0 .. k0 + 3]
+    // dX's column of this lane (its W1 fragments are loaded after the staging
+    // barrier, below)
     const int ct4 = w % NCT;
     const int kh = w / NCT;
     const int col = chunk * kHdxCols + ct4 * 16 + i16;
-    const float* w1row = W1 + (int64_t)min(col, in_features - 1) * hidden;
-    floatx4 wb[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        wb[g] = *reinterpret_cast<const floatx4*>(w1row + min(kh * KH + 16 * g + 4 * q, hidden - 4));
-    }
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
         const int e = u * kHdxThreads + t;
@@ -589,6 +585,16 @@ mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
     lbls[t & (kHdxRows - 1)] = lab_t;
     b2s[t & (CM - 1)] = (t & (CM - 1)) < classes ? b2_t : 0.0f;
     __syncthreads();
+    // dX operand b: W1[col][k0 .. k0 + 3].  Issued after the barrier, where
+    // the head's own loads are in: issued at the start with them, these 64 KB
+    // per block competed with them (16.52 -> 16.37 us per step), and issued
+    // after the z products' barrier they arrived late for dX (16.64 us).
+    const float* w1row = W1 + (int64_t)min(col, in_features - 1) * hidden;
+    floatx4 wb[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        wb[g] = *reinterpret_cast<const floatx4*>(w1row + min(kh * KH + 16 * g + 4 * q, hidden - 4));
+    }
 
     // ---- z = H W2: this wave's 32 hidden values ----
     const floatx4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
