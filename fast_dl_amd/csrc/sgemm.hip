@@ -2441,8 +2441,10 @@ struct JobGemm {
     }
 };
 
-// A kGemm16 job: four waves of 64 k each, all of a wave's k in flight.
-constexpr int kGroupITS16 = 4;
+// A kGemm16 job: four waves of split K, two 16-k groups of loads in flight
+// per register buffer (MLP step with all four of a wave's groups at once:
+// 16.36 -> 16.29 us per step; one group per buffer: 16.35 us).
+constexpr int kGroupITS16 = 2;
 template <bool TA, bool TB, bool VA, bool VB>
 struct JobGemm16 {
     static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
