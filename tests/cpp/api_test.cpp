@@ -461,6 +461,39 @@ int main() {
         return ok;
     });
 
+    run("mlp2_multi_step_graph_matches_eager_steps", [] {
+        // A graph of three steps replayed twice: six eager steps' parameters
+        // and last loss, bit for bit; steps < 1 is refused.
+        const int batch = 64, in = 32, hidden = 16, classes = 10;
+        dl::train::Mlp2 eager(in, hidden, classes, batch, kDev, 7);
+        dl::train::Mlp2 graphed(in, hidden, classes, batch, kDev, 7);
+        auto x = dl::Tensor::from_host<float>(randv(batch * in, 23, 0, 1), dl::Shape({batch, in}), kDev);
+        std::vector<int64_t> lab(batch);
+        for (int i = 0; i < batch; ++i) lab[i] = (i * 7 + 2) % classes;
+        auto labels = dl::Tensor::from_host<int64_t>(lab, dl::Shape({batch}), kDev);
+        bool threw = false;
+        try {
+            graphed.capture(x, labels, 0.25f, 0);
+        } catch (const std::runtime_error&) {
+            threw = true;
+        }
+        dl::Stream s(kDev);
+        dl::StreamGuard g(s);
+        graphed.capture(x, labels, 0.25f, 3);
+        bool ok = threw;
+        for (int rep = 0; rep < 2; ++rep) {
+            float le = 0.0f;
+            for (int i = 0; i < 3; ++i) le = eager.step(x, labels, 0.25f);
+            const float lg = graphed.replay();
+            ok = ok && std::isfinite(le) && le == lg;
+        }
+        ok = ok && eager.w1().to_host<float>() == graphed.w1().to_host<float>() &&
+             eager.b1().to_host<float>() == graphed.b1().to_host<float>() &&
+             eager.w2().to_host<float>() == graphed.w2().to_host<float>() &&
+             eager.b2().to_host<float>() == graphed.b2().to_host<float>();
+        return ok;
+    });
+
     // The block cache: a tensor allocated on stream T and freed while S is
     // current goes back to T, so S cannot overwrite it under T's queued work.
     run("allocator_freed_block_returns_to_home_stream", [] {
