@@ -1807,7 +1807,9 @@ sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
 // ---------------------------------------------------------------------------
 template <int KW, int KC>
 __global__ void __launch_bounds__(KW * 64)
-sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
+sgemm_splitk16_lds_kernel(const float* __restrict__ A0, const float* __restrict__ B0,
+                          int64_t strideA, int64_t strideB, int lda, int ldb, int M, int N, int K,
+                          GemmParams p) {
     constexpr int GR = KC / 16;           // k groups of a wave
     static_assert(KC == 64 && GR == 4, "copy counts and waits assume KC = 64 (four groups)");
     // One array per k group (A's 16 x 16 floats, then B's 16 x 16), so that
@@ -1826,33 +1828,24 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
     const int q = lane >> 4;
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    // (the grid is exactly the tiles: their count stands in for gridDim.x,
+    // which would be a scalar load from the dispatch's implicit arguments)
+    const int tiles_m = (M + 15) / 16, tiles_n = (N + 15) / 16;
+    tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * 16;
     const int n0 = tn * 16;
     const int64_t bz = blockIdx.y;
-    const float* __restrict__ A = p.A + bz * p.strideA;
-    const float* __restrict__ B = p.B + bz * p.strideB;
-    float* __restrict__ C = p.C + bz * p.strideC;
-    const float* __restrict__ aux = p.aux ? p.aux + bz * p.strideC : nullptr;
-    float* __restrict__ upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+    // The operands' shape and addresses come as leading scalar arguments,
+    // which the kernel receives preloaded in SGPRs; fields of the GemmParams
+    // aggregate are not preloaded, and the copies would wait for a scalar
+    // load of them.  `p` supplies the rest (C, the epilogue).
+    const float* __restrict__ A = A0 + bz * strideA;
+    const float* __restrict__ B = B0 + bz * strideB;
 
-    // The epilogue's elements of this thread and their extra operand
-    // (see epilogue_operand), loaded first so that the copies' waits below
-    // count copies only.  nw >= 4 (K > 768): one element per thread of the
-    // first four waves.
-    constexpr int kEpi = 1;
-    float pre[kEpi];
-#pragma unroll
-    for (int u = 0; u < kEpi; ++u) {
-        const int e = tid;
-        const int r = e / kWave;
-        const int ln = e % kWave;
-        const int gi = min(m0 + 4 * (ln >> 4) + r, p.M - 1);
-        const int gj = min(n0 + (ln & 15), p.N - 1);
-        pre[u] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
-    }
-
-    const int nw = blockDim.x / kWave;
+    // The block has exactly one wave per KC of K (the launch sizes it so), so
+    // every wave's K range starts inside K.  (The count comes from K rather
+    // than blockDim.x, another scalar load from the implicit arguments.)
+    const int nw = (K + KC - 1) / KC;
     const int kbeg = wave * KC;
     auto region = [&](auto gc) -> float* {
         constexpr int g = decltype(gc)::value;
@@ -1861,61 +1854,89 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
         else if constexpr (g == 2) return lg2[wave];
         else return lg3[wave];
     };
+    // The epilogue's element of this thread (the first four waves) and its
+    // extra operand (see epilogue_operand), loaded after the copies: its
+    // address needs the aggregate's fields, and the copies need only the
+    // preloaded arguments.
+    constexpr int kEpi = 1;
+    float pre[kEpi];
+    float* __restrict__ C = nullptr;
+    const float* __restrict__ aux = nullptr;
+    float* __restrict__ upd = nullptr;
+    auto load_pre = [&]() {
+        // (the barrier keeps the wait for the aggregate's fields after the
+        // copies: scheduled earlier, it would hold them back)
+        __builtin_amdgcn_sched_barrier(0);
+        C = p.C + bz * p.strideC;
+        aux = p.aux ? p.aux + bz * p.strideC : nullptr;
+        upd = p.upd ? p.upd + bz * p.strideC : nullptr;
+#pragma unroll
+        for (int u = 0; u < kEpi; ++u) {
+            const int e = tid;
+            const int r = e / kWave;
+            const int ln = e % kWave;
+            const int gi = min(m0 + 4 * (ln >> 4) + r, M - 1);
+            const int gj = min(n0 + (ln & 15), N - 1);
+            pre[u] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
+        }
+    };
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (kbeg < p.K) {
+    {
         // Copies in group order, A's then B's of each group, so group g has
         // landed once at most 2 (GR - 1 - g) copies are outstanding.
         const int ar = lane >> 2;             // A: row of this lane's chunk
         const int aq = lane & 3;              // A: slot within the row's group
         const int ac = aq ^ kc_swz<4>(ar);    // A: the chunk (k / 4 in the group) it holds
-        const int arow = min(m0 + ar, p.M - 1) - m0;
+        const int arow = min(m0 + ar, M - 1) - m0;
         const int sr = lane >> 2;             // B: slot row of the group
         const int kr = 4 * (sr & 3) + (sr >> 2);
-        const int bcol = min(n0 + 4 * (lane & 3), p.N - 4) - n0;
+        const int bcol = min(n0 + 4 * (lane & 3), N - 4) - n0;
         // Buffer copies from wave-uniform bases (the block's first row of A,
         // the wave's first k row of B); the lane parts are 32-bit offsets
         // (the host keeps 16 rows of A and 64 rows of B below 2 GiB).
-        const __amdgpu_buffer_rsrc_t ra = dma_buffer(wave_uniform(A + (int64_t)m0 * p.lda));
+        const __amdgpu_buffer_rsrc_t ra = dma_buffer(wave_uniform(A + (int64_t)m0 * lda));
         const __amdgpu_buffer_rsrc_t rb =
-            dma_buffer(wave_uniform(B + (int64_t)kbeg * p.ldb + n0));
+            dma_buffer(wave_uniform(B + (int64_t)kbeg * ldb + n0));
         auto copy = [&](auto gc) {
             constexpr int g = decltype(gc)::value;
-            const int gk = min(kbeg + 16 * g + 4 * ac, p.K - 4);
-            dma_buf_copy16(ra, (uint32_t)((int64_t)arow * p.lda + gk) * 4u, region(gc));
-            const int bk = min(kbeg + 16 * g + kr, p.K - 1) - kbeg;
-            dma_buf_copy16(rb, (uint32_t)((int64_t)bk * p.ldb + bcol) * 4u,
+            const int gk = min(kbeg + 16 * g + 4 * ac, K - 4);
+            dma_buf_copy16(ra, (uint32_t)((int64_t)arow * lda + gk) * 4u, region(gc));
+            const int bk = min(kbeg + 16 * g + kr, K - 1) - kbeg;
+            dma_buf_copy16(rb, (uint32_t)((int64_t)bk * ldb + bcol) * 4u,
                            region(gc) + 4 * kWave);
         };
         copy(std::integral_constant<int, 0>{});
         copy(std::integral_constant<int, 1>{});
         copy(std::integral_constant<int, 2>{});
         copy(std::integral_constant<int, 3>{});
+        load_pre();
         // Nothing may move between the copies and the waits below.
         __builtin_amdgcn_sched_barrier(0);
         // Group g's MFMAs start as soon as its two copies have landed.  Loads
-        // complete in order and the epilogue operand was loaded before the
-        // copies, so once at most 2 (GR - 1 - g) operations (the later
-        // groups' copies) are outstanding, group g's have landed; the wait is
-        // written here rather than left to the compiler, which places the
-        // same one only because it tells the four arrays apart.
+        // complete in order and the epilogue operand was loaded after the
+        // copies, so once at most 2 (GR - 1 - g) + 1 operations (the later
+        // groups' copies and that load) are outstanding, group g's have
+        // landed; the wait is written here rather than left to the compiler,
+        // which places the same one only because it tells the four arrays
+        // apart.
         auto group = [&](auto gc) {
             constexpr int g = decltype(gc)::value;
             // (the barrier keeps the scheduler from lifting this wait above
             // the previous group's MFMAs)
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (GR - 1 - g)));
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (GR - 1 - g) + 1));
             const int k0 = kbeg + 16 * g;
-            if (k0 >= p.K) return;
+            if (k0 >= K) return;
             const float* as = region(gc);
             const float* bs = as + 4 * kWave;
             floatx4 a = *reinterpret_cast<const floatx4*>(as + i * 16 + 4 * (q ^ kc_swz<4>(i)));
             float b[4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) b[st] = bs[(4 * st + q) * 16 + i];
-            if (k0 + 16 > p.K) {
+            if (k0 + 16 > K) {
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const bool in = k0 + 4 * q + st < p.K;
+                    const bool in = k0 + 4 * q + st < K;
                     a[st] = in ? a[st] : 0.0f;
                     b[st] = in ? b[st] : 0.0f;
                 }
@@ -1944,7 +1965,7 @@ sgemm_splitk16_lds_kernel(GemmParams p, int tiles_m, int tiles_n) {
         for (int w = 0; w < nw; ++w) v += red[w][r][ln];
         const int gi = m0 + 4 * (ln >> 4) + r;
         const int gj = n0 + (ln & 15);
-        if (gi < p.M && gj < p.N) {
+        if (gi < M && gj < N) {
             store_epilogue_pre(v, p, C, upd, (int64_t)gi * p.ldc + gj, pre[u]);
         }
     }
@@ -2552,7 +2573,8 @@ hipError_t launch_splitk16(const GemmParams& p, bool ta, bool tb, bool va, bool 
         const dim3 grid(((p.M + 15) / 16) * ((p.N + 15) / 16), nbatch);
         const int waves = (p.K + 63) / 64;  // 13 to 16
         hipLaunchKernelGGL((sgemm_splitk16_lds_kernel<16, 64>), grid, dim3(waves * kWave), 0,
-                           stream, p, (p.M + 15) / 16, (p.N + 15) / 16);
+                           stream, p.A, p.B, p.strideA, p.strideB, (int)p.lda, (int)p.ldb, p.M,
+                           p.N, p.K, p);
         return hipGetLastError();
     }
     if (p.K >= 512) return launch_splitk16_kw<16, 1>(p, ta, tb, va, vb, nbatch, stream);
