@@ -508,11 +508,14 @@ constexpr int kWave = 64;
 
 template <int CT>
 __global__ void __launch_bounds__(kHdxThreads)
-mlp_head_dx_kernel(const float* __restrict__ H, const float* __restrict__ W2,
+mlp_head_dx_kernel(int batch, int in_features, int hidden, int classes,
+                   const float* __restrict__ H, const float* __restrict__ W2,
                    const float* __restrict__ b2, const int64_t* __restrict__ labels,
                    const float* __restrict__ W1, float* __restrict__ logits,
-                   float* __restrict__ G2, float* __restrict__ G1, float* __restrict__ dX,
-                   int batch, int in_features, int hidden, int classes) {
+                   float* __restrict__ G2, float* __restrict__ G1, float* __restrict__ dX) {
+    // (the shape and the loaded operands lead the arguments: the first 14
+    // dwords arrive preloaded in SGPRs, so the first loads' addresses wait
+    // for no scalar load of the rest)
     constexpr int CM = 16 * CT;                  // classes padded to whole tiles
     constexpr int JR = 256;                      // hidden <= JR
     constexpr int LR = CM + 4;                   // w2s row stride: the 16 rows of a
@@ -919,13 +922,13 @@ hipError_t launch_mlp_head_dx(const float* H, const float* W2, const float* b2,
     const dim3 grid((unsigned)((in_features + kHdxCols - 1) / kHdxCols),
                     (unsigned)((batch + kHdxRows - 1) / kHdxRows));
     if (classes <= 16) {
-        hipLaunchKernelGGL((mlp_head_dx_kernel<1>), grid, dim3(kHdxThreads), 0, stream, H, W2,
-                           b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
-                           (int)hidden, (int)classes);
+        hipLaunchKernelGGL((mlp_head_dx_kernel<1>), grid, dim3(kHdxThreads), 0, stream,
+                           (int)batch, (int)in_features, (int)hidden, (int)classes, H, W2, b2,
+                           labels, W1, logits, G2, G1, dX);
     } else {
-        hipLaunchKernelGGL((mlp_head_dx_kernel<2>), grid, dim3(kHdxThreads), 0, stream, H, W2,
-                           b2, labels, W1, logits, G2, G1, dX, (int)batch, (int)in_features,
-                           (int)hidden, (int)classes);
+        hipLaunchKernelGGL((mlp_head_dx_kernel<2>), grid, dim3(kHdxThreads), 0, stream,
+                           (int)batch, (int)in_features, (int)hidden, (int)classes, H, W2, b2,
+                           labels, W1, logits, G2, G1, dX);
     }
     return hipGetLastError();
 }

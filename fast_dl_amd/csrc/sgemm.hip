@@ -1531,7 +1531,12 @@ __device__ __forceinline__ void splitk_load_group(const float* __restrict__ A,
 // The body takes its block index and the number of blocks that share the
 // tile mapping explicitly, so a grouped launch can run it on a sub-range of
 // its grid (sgemm_group_kernel).
-template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
+// LATE_PRE issues the epilogue's operand loads after the first super-chunk's
+// loads instead of before them: for a caller whose shape and operand
+// addresses arrive in SGPRs, the epilogue's fields (C, its extra operand, the
+// epilogue kind) are then the only scalar loads, and nothing waits for them
+// before the first loads are issued.
+template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB, bool LATE_PRE = false>
 __device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, int tiles_n,
                                               int kchunk, int bid, int nblocks, int64_t bz) {
     __shared__ float red[KW][16][kWave];
@@ -1569,20 +1574,23 @@ __device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, 
     // fetched now (see epilogue_operand).
     constexpr int kEpi = (16 * kWave + KW * kWave - 1) / (KW * kWave);
     float pre[kEpi];
+    auto load_pre = [&]() {
 #pragma unroll
-    for (int q = 0; q < kEpi; ++q) {
-        const int e = tid + q * KW * kWave;
-        const int r = e / kWave;
-        const int ln = e % kWave;
-        // Clamped into C rather than branched around: a lane-divergent branch
-        // around the load makes both of its sides load into one register,
-        // and the compiler then waits for the first before the K loop's
-        // loads are even issued.  Out-of-range lanes load a valid element
-        // they never store.
-        const int gi = min(m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), p.M - 1);
-        const int gj = min(n0 + (ln & 31), p.N - 1);
-        pre[q] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
-    }
+        for (int q = 0; q < kEpi; ++q) {
+            const int e = tid + q * KW * kWave;
+            const int r = e / kWave;
+            const int ln = e % kWave;
+            // Clamped into C rather than branched around: a lane-divergent
+            // branch around the load makes both of its sides load into one
+            // register, and the compiler then waits for the first before the
+            // K loop's loads are even issued.  Out-of-range lanes load a
+            // valid element they never store.
+            const int gi = min(m0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), p.M - 1);
+            const int gj = min(n0 + (ln & 31), p.N - 1);
+            pre[q] = epilogue_operand(p, C, aux, upd, (int64_t)gi * p.ldc + gj, gj);
+        }
+    };
+    if constexpr (!LATE_PRE) load_pre();
 
     floatx16 acc;
 #pragma unroll
@@ -1614,6 +1622,7 @@ __device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, 
     };
 
     if (supers > 0) load_super(0, a0, b0);
+    if constexpr (LATE_PRE) load_pre();
     for (int sc = 0; sc < supers; sc += 2) {
         if (sc + 1 < supers) load_super(sc + 1, a1, b1);
         mfma_super(a0, b0);
@@ -2454,11 +2463,36 @@ struct GroupArgs {
 constexpr int kGroupKW = 4;   // split-K waves of a grouped GEMM job (256 threads)
 constexpr int kGroupITS = 8;  // 64 k of loads per wave in flight (MLP step 22.5 -> 21.9 us)
 
+// Job 0's block count, and for a GEMM job 0 its shape and operand
+// addresses: the grouped kernel takes them as leading scalar arguments,
+// which arrive preloaded in SGPRs (the compiler preloads leading arguments
+// that are not aggregates), so the first job's first loads wait for no
+// scalar load of the GroupArgs aggregate.
+struct GroupLead {
+    const float* A;
+    const float* B;
+    int lda, ldb, M, N, K, tiles_m, tiles_n, kchunk, blocks;
+};
+
 template <bool TA, bool TB, bool VA, bool VB>
 struct JobGemm {
     static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
         splitk32_body<kGroupKW, kGroupITS, TA, TB, VA, VB>(a.p, a.tiles_m, a.tiles_n, a.kchunk,
                                                            bid, a.blocks, 0);
+    }
+    // As job 0: the lead's fields in place of the aggregate's.
+    static __device__ __forceinline__ void run_first(const GroupLead& l, const GroupDev& a,
+                                                     int bid) {
+        GemmParams p = a.p;
+        p.A = l.A;
+        p.B = l.B;
+        p.lda = l.lda;
+        p.ldb = l.ldb;
+        p.M = l.M;
+        p.N = l.N;
+        p.K = l.K;
+        splitk32_body<kGroupKW, kGroupITS, TA, TB, VA, VB, true>(p, l.tiles_m, l.tiles_n,
+                                                                 l.kchunk, bid, l.blocks, 0);
     }
 };
 
@@ -2477,6 +2511,10 @@ struct JobGemm16 {
 struct JobColsumSgd {
     static __device__ __forceinline__ void run(const GroupDev& a, int bid) {
         colsum_body(a.x, a.out, a.param, a.lr, a.rows, a.cols, bid);
+    }
+    static __device__ __forceinline__ void run_first(const GroupLead&, const GroupDev& a,
+                                                     int bid) {
+        run(a, bid);
     }
 };
 
@@ -2520,11 +2558,20 @@ __device__ __forceinline__ void group_dispatch(const GroupArgs& a, int bid) {
     }
 }
 
-template <class... J>
+template <class J0, class... Rest>
 __global__ void __launch_bounds__(kGroupKW * kWave)
-sgemm_group_kernel(GroupArgs a) {
-    static_assert(sizeof...(J) >= 2 && sizeof...(J) <= kGroupMaxJobs, "2 to 4 jobs");
-    group_dispatch<0, J...>(a, blockIdx.x);
+sgemm_group_kernel(const float* __restrict__ A0, const float* __restrict__ B0, int lda0,
+                   int ldb0, int M0, int N0, int K0, int tiles_m0, int tiles_n0, int kchunk0,
+                   int blocks0, GroupArgs a) {
+    static_assert(sizeof...(Rest) >= 1 && sizeof...(Rest) < kGroupMaxJobs, "2 to 4 jobs");
+    const int bid = blockIdx.x;
+    if (bid < blocks0) {
+        const GroupLead lead{A0, B0, lda0, ldb0, M0, N0, K0, tiles_m0, tiles_n0, kchunk0,
+                             blocks0};
+        J0::run_first(lead, a.d[0], bid);
+    } else {
+        group_dispatch<1, Rest...>(a, bid - blocks0);
+    }
 }
 
 template <int KW, int ITS = 1>
@@ -2987,8 +3034,10 @@ template <class... J>
 hipError_t launch_group_of(const GroupArgs& a, hipStream_t stream) {
     int blocks = 0;
     for (int i = 0; i < (int)sizeof...(J); ++i) blocks += a.d[i].blocks;
+    const GroupDev& d0 = a.d[0];
     hipLaunchKernelGGL((sgemm_group_kernel<J...>), dim3(blocks), dim3(kGroupKW * kWave), 0,
-                       stream, a);
+                       stream, d0.p.A, d0.p.B, (int)d0.p.lda, (int)d0.p.ldb, d0.p.M, d0.p.N,
+                       d0.p.K, d0.tiles_m, d0.tiles_n, d0.kchunk, d0.blocks, a);
     return hipGetLastError();
 }
 
@@ -3015,6 +3064,8 @@ hipError_t launch_group(const GroupJob* jobs, int n, hipStream_t stream) {
             (j.p.M <= 0 || j.p.N <= 0 || j.p.K <= 0)) {
             return hipErrorInvalidValue;
         }
+        // (the first job's leading dimensions travel as 32-bit kernel arguments)
+        if (i == 0 && (j.p.lda > INT32_MAX || j.p.ldb > INT32_MAX)) return hipErrorInvalidValue;
         if (j.kind == GroupJob::kHeadFinalize &&
             (j.rows <= 0 || j.cols <= 0 || j.cols > kColsumCols)) {
             return hipErrorInvalidValue;
