@@ -873,9 +873,32 @@ __device__ __forceinline__ void flat_batch_coords(int bid, int nblocks, int tile
     tn = t / tiles_m;
 }
 
+// The operands' addresses, batch strides, leading dimensions and shape, the
+// bias and the epilogue kind come as leading scalar arguments, which arrive
+// preloaded in SGPRs (14 dwords; the compiler preloads only leading
+// arguments that are not aggregates): the bias load and the first copies
+// then wait for no scalar load of the GemmParams aggregate, which supplies
+// only what the epilogue needs.  `mode` holds the epilogue kind in its low 8
+// bits and, for a 1-D grid over every tile of every batch (few tiles per
+// batch, see flat_batch_coords), the batch count above them (0: grid.y is
+// the batch and grid.x the tiles).
 template <class Cfg, bool TA, bool TB>
 __global__ void __launch_bounds__(Cfg::NT, Cfg::WPE)
-sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
+sgemm_dma_kernel(const float* __restrict__ A0, const float* __restrict__ B0,
+                 const float* __restrict__ bias, int strideA, int strideB, int lda, int ldb, int M,
+                 int N, int K, int mode, GemmParams pa) {
+    GemmParams p = pa;
+    p.A = A0;
+    p.B = B0;
+    p.bias = bias;
+    p.strideA = strideA;
+    p.strideB = strideB;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.epilogue = mode & 255;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, WM = Cfg::WM, WN = Cfg::WN;
     constexpr int NT = Cfg::NT, S = Cfg::STAGES;
     constexpr int FM = WM / 32, FN = WN / 32, WGM = BM / WM;
@@ -905,12 +928,18 @@ sgemm_dma_kernel(GemmParams p, int tiles_m, int tiles_n, int flat) {
     const int wn0 = (wmn / WGM) * WN;
     const int g0 = kset * NGK;                  // this set's first k-group of a tile
 
+    // (the tile counts and the grid's size follow from the shape: gridDim.x
+    // would be a scalar load from the dispatch's implicit arguments)
+    const int tiles_m = (M + BM - 1) / BM;
+    const int tiles_n = (N + BN - 1) / BN;
+    const int flat_batches = mode >> 8;
     int tm, tn;
     int64_t bz;
-    if (flat) {
-        flat_batch_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn, bz);
+    if (flat_batches) {
+        flat_batch_coords(blockIdx.x, tiles_m * tiles_n * flat_batches, tiles_m, tiles_n, tm, tn,
+                          bz);
     } else {
-        tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+        tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
         bz = blockIdx.y;
     }
     const int m0 = tm * BM;
@@ -2349,25 +2378,43 @@ constexpr int kFlatBatchMaxTiles = 64;
 
 template <class Cfg>
 hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStream_t stream) {
+    // The kernel takes the batch strides as 32-bit arguments: a batch whose
+    // stride does not fit runs one problem per launch.
+    if (nbatch > 1 && (p.strideA > INT32_MAX || p.strideB > INT32_MAX)) {
+        for (int b = 0; b < nbatch; ++b) {
+            GemmParams q = p;
+            q.A += b * p.strideA;
+            q.B += b * p.strideB;
+            q.C += b * p.strideC;
+            if (q.aux) q.aux += b * p.strideC;
+            if (q.upd) q.upd += b * p.strideC;
+            const hipError_t err = launch_dma<Cfg>(q, ta, tb, 1, stream);
+            if (err != hipSuccess) return err;
+        }
+        return hipSuccess;
+    }
     const int tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     const int tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const int tiles = tiles_m * tiles_n;
-    const int flat = nbatch > 1 && tiles <= kFlatBatchMaxTiles;
+    const bool flat = nbatch > 1 && tiles <= kFlatBatchMaxTiles;
     const dim3 grid = flat ? dim3(tiles * nbatch) : dim3(tiles, nbatch);
     const dim3 block(Cfg::NT);
+    const int sa = nbatch > 1 ? (int)p.strideA : 0;
+    const int sb = nbatch > 1 ? (int)p.strideB : 0;
+    const int mode = p.epilogue | (flat ? nbatch << 8 : 0);
+#define FDL_DMA_LAUNCH(TA_, TB_)                                                              \
+    hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, TA_, TB_>), grid, block, 0, stream, p.A, p.B,   \
+                       p.bias, sa, sb, (int)p.lda, (int)p.ldb, p.M, p.N, p.K, mode, p)
     if (!ta && !tb) {
-        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, false>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n, flat);
+        FDL_DMA_LAUNCH(false, false);
     } else if (!ta) {
-        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, false, true>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n, flat);
+        FDL_DMA_LAUNCH(false, true);
     } else if (!tb) {
-        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, true, false>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n, flat);
+        FDL_DMA_LAUNCH(true, false);
     } else {
-        hipLaunchKernelGGL((sgemm_dma_kernel<Cfg, true, true>), grid, block, 0, stream, p,
-                           tiles_m, tiles_n, flat);
+        FDL_DMA_LAUNCH(true, true);
     }
+#undef FDL_DMA_LAUNCH
     return hipGetLastError();
 }
 

@@ -173,6 +173,34 @@ def test_batched_broadcast_and_padded_ld(device):
         check_gemm(np.ascontiguousarray(c[:, :, :N]), 0, 0, Ap, Bp, M, N, K, batch=batch)
 
 
+@pytest.mark.parametrize("fam", ["dma64", "dma64s"])
+def test_dma_batch_stride_beyond_int32(device, fam):
+    # The direct-to-LDS kernels take batch strides as 32-bit arguments; a
+    # stride past 2^31 - 1 runs one problem per launch.  A's two problems sit
+    # 2^31 + 256 floats (8 GiB) apart in one allocation, B is shared.
+    import torch
+
+    kernel = {"dma64": capi.KERNEL_DMA64, "dma64s": capi.KERNEL_DMA64S}[fam]
+    g = rng(9)
+    batch, M, N, K = 2, 64, 64, 64
+    A = g.standard_normal((batch, M, K)).astype(np.float32)
+    B = g.standard_normal((1, K, N)).astype(np.float32)
+    sA = (1 << 31) + 256
+    big = torch.empty(sA + M * K, device="cuda")
+    big[: M * K] = dev(A[0]).reshape(-1)
+    big[sA : sA + M * K] = dev(A[1]).reshape(-1)
+    dB = dev(B)
+    dC = torch.full((batch, M, N), float("nan"), device="cuda")
+    say(f"stride beyond int32 fam={fam}")
+    capi.sgemm_ex_select(0, 0, M, N, K, big.data_ptr(), K, sA, dB.data_ptr(), N, 0,
+                         dC.data_ptr(), N, M * N, batch, None, None, 0, kernel, stream())
+    c = host(dC)
+    del big
+    torch.cuda.empty_cache()
+    check_gemm(c, 0, 0, A, np.ascontiguousarray(np.broadcast_to(B, (batch, K, N))), M, N, K,
+               batch=batch)
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
 def test_skinny_vs_oracle(device, M):
     g = rng(50 + M)
