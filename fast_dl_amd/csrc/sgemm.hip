@@ -2136,9 +2136,14 @@ constexpr int kSplitWaves = 4;
 constexpr int kPartMaxRows = 512;  // slice rows whose A values the partial pass stages in LDS
 constexpr int64_t kSplitMinElems = int64_t(1) << 23;   // 32 MB of B
 
+// The pass takes only scalar arguments, which arrive preloaded in SGPRs (a
+// GemmParams aggregate's fields would be scalar loads that the first loads
+// wait for); `tiles` is the grid's size (bands x S).
 template <int MR, bool TA, int UNR>
 __global__ void __launch_bounds__(kSplitWaves * kWave)
-sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part) {
+sgemm_skinny_part_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                         float* __restrict__ part, int lda, int ldb, int M, int N, int K, int S,
+                         int rows, int tiles) {
     constexpr int NW = kSplitWaves;
     __shared__ float red[NW][MR][kSplitBand];
     // A's slice for MR > 2 (see below); MR <= 2 keeps A in scalar loads
@@ -2148,20 +2153,16 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
     // wave-uniform, so A's loads below have wave-uniform addresses
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
 
-    const int tiles = gridDim.x;
     int t = blockIdx.x;
     // each XCD takes a contiguous range of (band, slice) tiles: whole bands
     if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
     const int band = t / S;
     const int slice = t - band * S;
     const int k0 = slice * rows;
-    const int k1 = min(k0 + rows, p.K);
+    const int k1 = min(k0 + rows, K);
     // N % 4 == 0 here; lanes past the edge re-read the last float4 and their
     // sums land only in partial slots that pass 2 never reads.
-    const int n0 = min(band * kSplitBand + lane * 4, p.N - 4);
-    const float* __restrict__ A = p.A;
-    const float* __restrict__ B = p.B;
-    const int M = p.M;
+    const int n0 = min(band * kSplitBand + lane * 4, N - 4);
 
     float acc[MR][4];
 #pragma unroll
@@ -2170,13 +2171,13 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
         for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
     auto a_at = [&](int m, int k) {
         const int mm = min(m, M - 1);
-        return TA ? A[(int64_t)k * p.lda + mm] : A[(int64_t)mm * p.lda + k];
+        return TA ? A[(int64_t)k * (int64_t)lda + mm] : A[(int64_t)mm * (int64_t)lda + k];
     };
 
     auto load = [&](int kk, floatx4 (&b)[UNR], float (&a)[UNR][MR]) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
-            b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * p.ldb + n0);
+            b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * (int64_t)ldb + n0);
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
 #pragma unroll
@@ -2237,7 +2238,7 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
         auto load_b = [&](int kk, floatx4 (&b)[UNR]) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
-                b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * p.ldb + n0);
+                b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * (int64_t)ldb + n0);
         };
         auto fma_lds = [&](int kk, const floatx4 (&b)[UNR]) {
 #pragma unroll
@@ -2275,7 +2276,7 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
         }
     }
     for (; k < k1; k += NW) {
-        const floatx4 b = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + n0);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(B + (int64_t)k * (int64_t)ldb + n0);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             const float a = a_at(m, k);
@@ -2304,11 +2305,13 @@ sgemm_skinny_part_kernel(GemmParams p, int S, int rows, float* __restrict__ part
 // last one and are not added), so the pass costs one memory round trip.
 template <int MR, int SMAX>
 __global__ void __launch_bounds__(kSplitBand)
-sgemm_skinny_sum_kernel(GemmParams p, int S, const float* __restrict__ part) {
+sgemm_skinny_sum_kernel(const float* __restrict__ part, int S, int N, GemmParams p) {
+    // (the partials' address, S and N lead the arguments, preloaded in SGPRs:
+    // the loads below wait for no scalar load of the aggregate)
     const int band = blockIdx.x;
     const int m = blockIdx.y;
     const int j = band * kSplitBand + (int)threadIdx.x;
-    if (j >= p.N) return;
+    if (j >= N) return;
     const float* __restrict__ src = part + ((int64_t)band * S * MR + m) * kSplitBand + threadIdx.x;
     float x[SMAX];
 #pragma unroll
@@ -2724,25 +2727,28 @@ hipError_t launch_skinny_split_mr(const GemmParams& p, bool ta, const SkinnySpli
     constexpr int UNR = 4;
     const dim3 grid1(s.bands * s.slices);
     const dim3 block1(kSplitWaves * kWave);
+    const int tiles = s.bands * s.slices;
     if (ta) {
         hipLaunchKernelGGL((sgemm_skinny_part_kernel<MR, true, UNR>), grid1, block1, 0, stream,
-                           p, s.slices, s.rows, part);
+                           p.A, p.B, part, (int)p.lda, (int)p.ldb, p.M, p.N, p.K, s.slices,
+                           s.rows, tiles);
     } else {
         hipLaunchKernelGGL((sgemm_skinny_part_kernel<MR, false, UNR>), grid1, block1, 0, stream,
-                           p, s.slices, s.rows, part);
+                           p.A, p.B, part, (int)p.lda, (int)p.ldb, p.M, p.N, p.K, s.slices,
+                           s.rows, tiles);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const dim3 grid2(s.bands, p.M);
     if (s.slices <= 16) {
         hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, 16>), grid2, dim3(kSplitBand), 0, stream,
-                           p, s.slices, part);
+                           part, s.slices, p.N, p);
     } else if (s.slices <= 32) {
         hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, 32>), grid2, dim3(kSplitBand), 0, stream,
-                           p, s.slices, part);
+                           part, s.slices, p.N, p);
     } else {
         hipLaunchKernelGGL((sgemm_skinny_sum_kernel<MR, kSplitMaxSlices>), grid2,
-                           dim3(kSplitBand), 0, stream, p, s.slices, part);
+                           dim3(kSplitBand), 0, stream, part, s.slices, p.N, p);
     }
     return hipGetLastError();
 }
@@ -3007,6 +3013,8 @@ SkinnySplit skinny_split_plan(const GemmParams& p, bool transA, bool transB, int
     SkinnySplit s;
     if (batch != 1 || choose_kernel(p, transA, transB, batch) != GemmKernel::Skinny) return s;
     if (p.M < 1 || p.N % 4 != 0 || p.K < 1) return s;
+    // (the partial pass takes its leading dimensions as 32-bit arguments)
+    if (p.lda > INT32_MAX || p.ldb > INT32_MAX) return s;
     // The second pass costs about 3 us.  It pays when each strip of the
     // single pass is long (K >= 4096: 1.1x at N = 4096, 1.35x at N = 1024,
     // 3.2x at N = 1024, K = 16384) or B is large (N = 16384, K = 1024:
