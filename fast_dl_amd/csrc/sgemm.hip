@@ -1684,11 +1684,30 @@ __device__ __forceinline__ void splitk32_body(const GemmParams& p, int tiles_m, 
     store_epilogue_elems<kEpi>(v, off, live, pre, p, C, upd);
 }
 
+// The operands' addresses, leading dimensions, 32-bit batch strides, shape and
+// K chunk come as leading scalar arguments, preloaded in SGPRs (14 dwords;
+// the compiler preloads only leading arguments that are not aggregates), so
+// the first loads wait for no scalar load of the GemmParams aggregate, which
+// supplies the epilogue's fields; its operand is loaded after the first loads
+// (LATE_PRE).  The tile counts and the grid's size follow from the shape.
 template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
 __global__ void __launch_bounds__(KW * 64)
-sgemm_splitk32_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
-    splitk32_body<KW, ITS, TA, TB, VA, VB>(p, tiles_m, tiles_n, kchunk, blockIdx.x, gridDim.x,
-                                           blockIdx.y);
+sgemm_splitk32_kernel(const float* __restrict__ A0, const float* __restrict__ B0, int64_t lda,
+                      int64_t ldb, int strideA, int strideB, int M, int N, int K, int kchunk,
+                      GemmParams pa) {
+    GemmParams p = pa;
+    p.A = A0;
+    p.B = B0;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.strideA = strideA;
+    p.strideB = strideB;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    const int tiles_m = (M + 31) / 32, tiles_n = (N + 31) / 32;
+    splitk32_body<KW, ITS, TA, TB, VA, VB, true>(p, tiles_m, tiles_n, kchunk, blockIdx.x,
+                                                 tiles_m * tiles_n, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -1816,9 +1835,25 @@ __device__ __forceinline__ void splitk16_body(const GemmParams& p, int tiles_m, 
 
 template <int KW, int ITS, bool TA, bool TB, bool VA, bool VB>
 __global__ void __launch_bounds__(KW * 64)
-sgemm_splitk16_kernel(GemmParams p, int tiles_m, int tiles_n, int kchunk) {
-    splitk16_body<KW, ITS, TA, TB, VA, VB>(p, tiles_m, tiles_n, kchunk, blockIdx.x, gridDim.x,
-                                           blockIdx.y);
+sgemm_splitk16_kernel(const float* __restrict__ A0, const float* __restrict__ B0, int64_t lda,
+                      int64_t ldb, int strideA, int strideB, int M, int N, int K, int kchunk,
+                      GemmParams pa) {
+    // (leading scalar arguments as sgemm_splitk32_kernel's; the epilogue's
+    // operand is loaded before the K range here: after the first loads it
+    // measured slower, 3.93 -> 4.09 us at 256x256x512 with bias+ReLU)
+    GemmParams p = pa;
+    p.A = A0;
+    p.B = B0;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.strideA = strideA;
+    p.strideB = strideB;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    const int tiles_m = (M + 15) / 16, tiles_n = (N + 15) / 16;
+    splitk16_body<KW, ITS, TA, TB, VA, VB>(p, tiles_m, tiles_n, kchunk, blockIdx.x,
+                                           tiles_m * tiles_n, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -2020,9 +2055,24 @@ sgemm_splitk16_lds_kernel(const float* __restrict__ A0, const float* __restrict_
 // band of B's columns.  Column and row indices are clamped into the matrices:
 // lanes past the edge load valid data that only reaches outputs never stored.
 // ---------------------------------------------------------------------------
+// The operands' addresses, leading dimensions, 32-bit batch strides, shape and
+// strip count lead the arguments, preloaded in SGPRs (see
+// sgemm_splitk32_kernel); the aggregate supplies the epilogue.
 template <int MR, bool TA, bool VB, int STRIP, int NT, int UNR>
 __global__ void __launch_bounds__(NT)
-sgemm_skinny_kernel(GemmParams p, int strips) {
+sgemm_skinny_kernel(const float* __restrict__ A0, const float* __restrict__ B0, int64_t lda,
+                    int64_t ldb, int strideA, int strideB, int M, int N, int K, int strips,
+                    GemmParams pa) {
+    GemmParams p = pa;
+    p.A = A0;
+    p.B = B0;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.strideA = strideA;
+    p.strideB = strideB;
+    p.M = M;
+    p.N = N;
+    p.K = K;
     constexpr int CW = VB ? 4 : 1;
     constexpr int CL = STRIP / CW;
     constexpr int KL = NT / CL;
@@ -2039,8 +2089,6 @@ sgemm_skinny_kernel(GemmParams p, int strips) {
     const float* __restrict__ B = p.B + bz * p.strideB;
     // VB: N % 4 == 0, so clamping to the last float4 keeps whole vectors.
     const int n0 = min(sid * STRIP + cl * CW, p.N - CW);
-    const int M = p.M;
-    const int K = p.K;
 
     float acc[MR][CW];
 #pragma unroll
@@ -2379,22 +2427,32 @@ hipError_t launch_tiled(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
 // larger ones keep grid.y = batch and the per-problem tile grouping.
 constexpr int kFlatBatchMaxTiles = 64;
 
+// Kernels that take the batch strides as 32-bit arguments run a batch whose
+// stride does not fit one problem per launch: launch(q) for each.
+inline bool strides_fit32(const GemmParams& p, int nbatch) {
+    return nbatch <= 1 || (p.strideA <= INT32_MAX && p.strideB <= INT32_MAX);
+}
+template <class F>
+hipError_t launch_per_problem(const GemmParams& p, int nbatch, F launch) {
+    for (int b = 0; b < nbatch; ++b) {
+        GemmParams q = p;
+        q.A += b * p.strideA;
+        q.B += b * p.strideB;
+        q.C += b * p.strideC;
+        if (q.aux) q.aux += b * p.strideC;
+        if (q.upd) q.upd += b * p.strideC;
+        const hipError_t err = launch(q);
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
+}
+
 template <class Cfg>
 hipError_t launch_dma(const GemmParams& p, bool ta, bool tb, int nbatch, hipStream_t stream) {
-    // The kernel takes the batch strides as 32-bit arguments: a batch whose
-    // stride does not fit runs one problem per launch.
-    if (nbatch > 1 && (p.strideA > INT32_MAX || p.strideB > INT32_MAX)) {
-        for (int b = 0; b < nbatch; ++b) {
-            GemmParams q = p;
-            q.A += b * p.strideA;
-            q.B += b * p.strideB;
-            q.C += b * p.strideC;
-            if (q.aux) q.aux += b * p.strideC;
-            if (q.upd) q.upd += b * p.strideC;
-            const hipError_t err = launch_dma<Cfg>(q, ta, tb, 1, stream);
-            if (err != hipSuccess) return err;
-        }
-        return hipSuccess;
+    if (!strides_fit32(p, nbatch)) {
+        return launch_per_problem(p, nbatch, [&](const GemmParams& q) {
+            return launch_dma<Cfg>(q, ta, tb, 1, stream);
+        });
     }
     const int tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     const int tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
@@ -2450,6 +2508,13 @@ hipError_t launch_dma_fit(const GemmParams& p, bool ta, bool tb, int nbatch, hip
 template <int KW, int ITS = 4>
 hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                               int nbatch, hipStream_t stream) {
+    if (!strides_fit32(p, nbatch)) {
+        return launch_per_problem(p, nbatch, [&](const GemmParams& q) {
+            return launch_splitk32_kw<KW, ITS>(q, ta, tb, va, vb, 1, stream);
+        });
+    }
+    const int sa = nbatch > 1 ? (int)p.strideA : 0;
+    const int sb = nbatch > 1 ? (int)p.strideB : 0;
     const int tiles_m = (p.M + 31) / 32;
     const int tiles_n = (p.N + 31) / 32;
     // K range per wave, a multiple of one super-chunk (8 * ITS steps), so only
@@ -2467,7 +2532,8 @@ hipError_t launch_splitk32_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
 #define FDL_SPLITK_CASE(C, TA_, TB_, VA_, VB_)                                          \
     case C:                                                                             \
         hipLaunchKernelGGL((sgemm_splitk32_kernel<KW, ITS, TA_, TB_, VA_, VB_>), grid,  \
-                           block, 0, stream, p, tiles_m, tiles_n, kchunk);              \
+                           block, 0, stream, p.A, p.B, p.lda, p.ldb, sa, sb, p.M, p.N,  \
+                           p.K, kchunk, p);                                             \
         break;
     switch (code) {
         FDL_SPLITK_CASE(0, false, false, false, false)
@@ -2627,6 +2693,13 @@ sgemm_group_kernel(const float* __restrict__ A0, const float* __restrict__ B0, i
 template <int KW, int ITS = 1>
 hipError_t launch_splitk16_kw(const GemmParams& p, bool ta, bool tb, bool va, bool vb,
                               int nbatch, hipStream_t stream) {
+    if (!strides_fit32(p, nbatch)) {
+        return launch_per_problem(p, nbatch, [&](const GemmParams& q) {
+            return launch_splitk16_kw<KW, ITS>(q, ta, tb, va, vb, 1, stream);
+        });
+    }
+    const int sa = nbatch > 1 ? (int)p.strideA : 0;
+    const int sb = nbatch > 1 ? (int)p.strideB : 0;
     const int tiles_m = (p.M + 15) / 16;
     const int tiles_n = (p.N + 15) / 16;
     constexpr int kSuper = 16 * ITS;
@@ -2640,7 +2713,8 @@ hipError_t launch_splitk16_kw(const GemmParams& p, bool ta, bool tb, bool va, bo
 #define FDL_SPLITK16_CASE(C, TA_, TB_, VA_, VB_)                                        \
     case C:                                                                             \
         hipLaunchKernelGGL((sgemm_splitk16_kernel<KW, ITS, TA_, TB_, VA_, VB_>), grid,  \
-                           block, 0, stream, p, tiles_m, tiles_n, kchunk);              \
+                           block, 0, stream, p.A, p.B, p.lda, p.ldb, sa, sb, p.M, p.N,  \
+                           p.K, kchunk, p);                                             \
         break;
     switch (code) {
         FDL_SPLITK16_CASE(0, false, false, false, false)
@@ -2691,16 +2765,27 @@ hipError_t launch_splitk32(const GemmParams& p, bool ta, bool tb, bool va, bool 
 template <int MR, int STRIP, int NT, int UNR>
 hipError_t launch_skinny_cfg(const GemmParams& p, bool ta, bool vb, int nbatch,
                              hipStream_t stream) {
+    if (!strides_fit32(p, nbatch)) {
+        return launch_per_problem(p, nbatch, [&](const GemmParams& q) {
+            return launch_skinny_cfg<MR, STRIP, NT, UNR>(q, ta, vb, 1, stream);
+        });
+    }
+    const int sa = nbatch > 1 ? (int)p.strideA : 0;
+    const int sb = nbatch > 1 ? (int)p.strideB : 0;
     const int strips = (p.N + STRIP - 1) / STRIP;
     const dim3 grid(strips, nbatch);
     const dim3 block(NT);
+#define FDL_SKINNY_LAUNCH(TA_, VB_)                                                         \
+    hipLaunchKernelGGL((sgemm_skinny_kernel<MR, TA_, VB_, STRIP, NT, UNR>), grid, block, 0, \
+                       stream, p.A, p.B, p.lda, p.ldb, sa, sb, p.M, p.N, p.K, strips, p)
     if (ta) {
-        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, true, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
-        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, true, false, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+        if (vb) FDL_SKINNY_LAUNCH(true, true);
+        else FDL_SKINNY_LAUNCH(true, false);
     } else {
-        if (vb) hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, true, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
-        else hipLaunchKernelGGL((sgemm_skinny_kernel<MR, false, false, STRIP, NT, UNR>), grid, block, 0, stream, p, strips);
+        if (vb) FDL_SKINNY_LAUNCH(false, true);
+        else FDL_SKINNY_LAUNCH(false, false);
     }
+#undef FDL_SKINNY_LAUNCH
     return hipGetLastError();
 }
 

@@ -173,16 +173,18 @@ def test_batched_broadcast_and_padded_ld(device):
         check_gemm(np.ascontiguousarray(c[:, :, :N]), 0, 0, Ap, Bp, M, N, K, batch=batch)
 
 
-@pytest.mark.parametrize("fam", ["dma64", "dma64s"])
-def test_dma_batch_stride_beyond_int32(device, fam):
-    # The direct-to-LDS kernels take batch strides as 32-bit arguments; a
-    # stride past 2^31 - 1 runs one problem per launch.  A's two problems sit
-    # 2^31 + 256 floats (8 GiB) apart in one allocation, B is shared.
+@pytest.mark.parametrize("fam", ["dma64", "dma64s", "splitk16", "splitk32", "skinny"])
+def test_batch_stride_beyond_int32(device, fam):
+    # These kernels take batch strides as 32-bit arguments; a stride past
+    # 2^31 - 1 runs one problem per launch.  A's two problems sit 2^31 + 256
+    # floats (8 GiB) apart in one allocation, B is shared.
     import torch
 
-    kernel = {"dma64": capi.KERNEL_DMA64, "dma64s": capi.KERNEL_DMA64S}[fam]
+    kernel = {"dma64": capi.KERNEL_DMA64, "dma64s": capi.KERNEL_DMA64S,
+              "splitk16": capi.KERNEL_SPLITK16, "splitk32": capi.KERNEL_SPLITK32,
+              "skinny": capi.KERNEL_SKINNY}[fam]
     g = rng(9)
-    batch, M, N, K = 2, 64, 64, 64
+    batch, M, N, K = 2, (8 if fam == "skinny" else 64), 64, 64
     A = g.standard_normal((batch, M, K)).astype(np.float32)
     B = g.standard_normal((1, K, N)).astype(np.float32)
     sA = (1 << 31) + 256
