@@ -324,8 +324,14 @@ def cpu_baseline_mlp(seconds=8.0):
                       f"{core}; host {cpu_model()}, {len(saved)} cpus visible"}
 
 
-def mlp_rate(capi, torch, steps=200, warmup=20):
-    """fdl_mlp2_train_step on BASELINE config 2 (784-256-10, batch 256), steps/s."""
+def mlp_rate(capi, torch, steps=2000, warmup=100):
+    """fdl_mlp2_train_step on BASELINE config 2 (784-256-10, batch 256), steps/s.
+
+    2000 steps (32 ms): the host issues a step in about 12 us and the GPU runs
+    one in about 16, so the queue fills after a start-up of a few hundred
+    microseconds, which 200 steps did not amortise (16.9-17.6 us per step
+    over 200 steps against 15.8 us over 1000 and 3000, measured in one
+    process)."""
     gen = torch.Generator(device="cuda").manual_seed(2)
     B, I, H, C = 256, 784, 256, 10
     X = torch.rand((B, I), generator=gen, device="cuda")
@@ -529,7 +535,7 @@ def sampled_parity(A, B, C, n, rows=16):
     return bool(np.all(np.abs(c - ref) <= bound))
 
 
-def torch_mlp_rate(torch, steps=200, warmup=20):
+def torch_mlp_rate(torch, steps=2000, warmup=100):
     """The same 784-256-10 step written in eager PyTorch (autograd, fused
     cross_entropy, torch.optim.SGD), for comparison only: steps/s."""
     gen = torch.Generator(device="cuda").manual_seed(2)
