@@ -3116,6 +3116,18 @@ SkinnySplit skinny_split_plan(const GemmParams& p, bool transA, bool transB, int
     int64_t slices = std::min<int64_t>(kSplitMaxSlices, (target + bands - 1) / bands);
     int64_t rows = (p.K + slices - 1) / slices;
     rows = std::max<int64_t>(64, (rows + 7) / 8 * 8);
+    // Slices that start a multiple of 4 MiB of B apart read the same HBM
+    // channels at the same time: 8 more rows per slice (the last slice
+    // shorter) spread them.  Graph-timed, M = 8: N = 4096, K = 8192 (256-row
+    // slices, 4 MiB apart) 37.7 -> 28.4 us; N = 16384, K = 1024 19.0 ->
+    // 16.4 us; N = 16384, K = 4096 58.0 -> 50.9 us; C5a (2 MiB apart)
+    // unchanged, and shifting 2 MiB strides as well made it slower (17.8 ->
+    // 18.6 us: the short last slice).  The workspace-size query has no ldb
+    // (0 here) and plans without the shift, which never takes fewer slices,
+    // so the size it returns covers the call's.
+    if (p.ldb > 0 && (rows * p.ldb * (int64_t)sizeof(float)) % (int64_t(4) << 20) == 0) {
+        rows += 8;
+    }
     slices = (p.K + rows - 1) / rows;
     if (slices < 2 || bands * slices > (1 << 22)) return s;
     s.mr = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : 8;

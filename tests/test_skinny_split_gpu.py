@@ -17,8 +17,11 @@ pytestmark = pytest.mark.gpu
 
 # (M, N, K, transA, epilogue): full bands and a part band, K slices of equal
 # and unequal length, 8 to 64 slices, M of every register-tile size (1, 2, 4,
-# 8) and between.
+# 8) and between, and two plans whose slices would start a multiple of 4 MiB
+# of B apart and take 8 more rows each instead (the last slice shorter).
 CASES = [
+    (8, 4096, 8192, 0, capi.EPILOGUE_BIAS_RELU),
+    (8, 16384, 1024, 0, capi.EPILOGUE_BIAS),
     (1, 4096, 4096, 0, capi.EPILOGUE_BIAS_RELU),
     (8, 4096, 4096, 0, capi.EPILOGUE_BIAS_RELU),
     (3, 1024, 4096, 1, capi.EPILOGUE_NONE),
@@ -52,7 +55,8 @@ def test_split_matches_fp64(device, M, N, K, ta, epi):
     assert np.array_equal(c, c2)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 8192), (3, 516, 20000)])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 8192), (3, 516, 20000),
+                                   (8, 4096, 8192)])
 def test_split_exact_on_integers(device, M, N, K):
     # integer operands in [-4, 4]: |partial sums| <= 16 K < 2^24, so every order is exact
     g = rng(17 + M + N)
