@@ -3106,13 +3106,16 @@ SkinnySplit skinny_split_plan(const GemmParams& p, bool transA, bool transB, int
     // 1.2x), not for shorter K at moderate size (N = 4096, K = 1024: 0.75x;
     // N = 1024, K = 2048: 0.94x).
     if (p.K < 4096 && (int64_t)p.N * p.K < kSplitMinElems) return s;
-    // About two rounds of the 256 CUs (1.5 at M <= 2), slices of at least 64
+    // About two rounds of the 256 CUs (1.6 at M <= 2), slices of at least 64
     // rows.  Blocks per launch, measured at K = N = 4096 (graph-timed, both
-    // passes): M = 1 14.8 us at 512 blocks, 14.5-14.6 at 384, 14.8 at 448,
-    // 15.3 at 320, 17.1 at 1024; M = 2 15.0 / 14.8 at 512 / 384; M = 4 and
-    // 8 were best at 512 (16.0 / 16.4 and 17.8 / 18.4).
+    // passes): M = 1 14.6-14.8 us at 512 blocks, 14.3-14.4 at 416, 15.1 at
+    // 400, 14.8 at 432 and at 448, 14.5-14.7 at 384, 15.3 at 320, 17.1 at
+    // 1024; M = 2 14.8-15.0 / 14.6 at 512 / 416; M = 4 and 8 were best at
+    // 512 (16.0 / 16.4 and 17.8 / 18.4 against 384).  The rate depends on
+    // where the slices start in B (see the 4 MiB rule below) as much as on
+    // the block count.
     const int64_t bands = (p.N + kSplitBand - 1) / kSplitBand;
-    const int64_t target = p.M <= 2 ? 384 : 512;
+    const int64_t target = p.M <= 2 ? 416 : 512;
     int64_t slices = std::min<int64_t>(kSplitMaxSlices, (target + bands - 1) / bands);
     int64_t rows = (p.K + slices - 1) / slices;
     rows = std::max<int64_t>(64, (rows + 7) / 8 * 8);
