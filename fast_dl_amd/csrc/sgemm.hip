@@ -2269,25 +2269,49 @@ sgemm_skinny_part_kernel(const float* __restrict__ A, const float* __restrict__ 
         // pipelined as above (with A in scalar loads the loop waited for all
         // of a group's MR * UNR A values, one cache round trip per group, and
         // a second set of them did not fit).  Same k order and sums, so the
-        // same bits.
-        const int nrows = k1 - k0;
-        for (int e = tid; e < nrows * MR; e += NW * kWave) {
-            int kk, m;
-            if (TA) {
-                kk = e / MR;  // A is K x M: consecutive e along m
-                m = e - kk * MR;
-            } else {
-                m = e / nrows;  // A is M x K: consecutive e along k
-                kk = e - m * nrows;
-            }
-            as_lds[kk * MR + m] = a_at(m, k0 + kk);
-        }
-        __syncthreads();
+        // same bits.  B's first rows are requested before the staging, so
+        // their round trip overlaps A's instead of following the barrier.
         auto load_b = [&](int kk, floatx4 (&b)[UNR]) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
                 b[u] = *reinterpret_cast<const floatx4*>(B + (int64_t)(kk + NW * u) * (int64_t)ldb + n0);
         };
+        const int span = k1 - k - NW * (UNR - 1);
+        const int groups = span > 0 ? (span + NW * UNR - 1) / (NW * UNR) : 0;
+        floatx4 b0[UNR], b1[UNR];
+        if (groups > 0) load_b(k, b0);
+        // A's slice, all of a thread's loads issued before its first store
+        // (one round trip): TA reads element e = tid + i * 256 as k row e / MR,
+        // column e % MR; otherwise row m = i / R, k = tid + 256 * (i % R).
+        const int nrows = k1 - k0;
+        constexpr int kThreads = NW * kWave;
+        constexpr int R = kPartMaxRows / kThreads;
+        constexpr int kStagePer = R * MR;
+        static_assert(kPartMaxRows % kThreads == 0, "staging rows in whole passes");
+        auto stage_pos = [&](int i, int& kk, int& m) {
+            if (TA) {
+                const int e = tid + i * kThreads;
+                kk = e / MR;
+                m = e % MR;
+            } else {
+                m = i / R;
+                kk = tid + (i % R) * kThreads;
+            }
+        };
+        float av[kStagePer];
+#pragma unroll
+        for (int i = 0; i < kStagePer; ++i) {
+            int kk, m;
+            stage_pos(i, kk, m);
+            av[i] = kk < nrows ? a_at(m, k0 + kk) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kStagePer; ++i) {
+            int kk, m;
+            stage_pos(i, kk, m);
+            if (kk < nrows) as_lds[kk * MR + m] = av[i];
+        }
+        __syncthreads();
         auto fma_lds = [&](int kk, const floatx4 (&b)[UNR]) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u) {
@@ -2298,10 +2322,6 @@ sgemm_skinny_part_kernel(const float* __restrict__ A, const float* __restrict__ 
                     for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(ar[m], b[u][c], acc[m][c]);
             }
         };
-        const int span = k1 - k - NW * (UNR - 1);
-        const int groups = span > 0 ? (span + NW * UNR - 1) / (NW * UNR) : 0;
-        floatx4 b0[UNR], b1[UNR];
-        if (groups > 0) load_b(k, b0);
         int it = 0;
         for (; it + 2 <= groups; it += 2) {
             load_b(k + NW * UNR, b1);
