@@ -644,6 +644,16 @@ __device__ __forceinline__ int kc_swz(int r) {
     return r & 15;  // 16 chunks: measured conflict-free, (r >> 1) & 15 costs 10%
 }
 
+// Chunk rotation of a k-contiguous tile of 16-float rows read by 16x16x4
+// MFMA fragments (lane l: row l % 16, chunk l / 16, one ds_read_b128).  A
+// ds_read_b128 is served in four passes of 16 lanes, lane l in the pass of
+// (l / 32, parity of bits 2..4 of l), each free of bank conflicts when its
+// lanes' 16-byte slots differ mod 16 (measured with the LDS bank-conflict
+// counter).  kc_swz<4>, right for the 32x32 fragments' lanes (32 rows x one
+// chunk), gives these lanes two-way conflicts; swapping the chunks of rows
+// 4..7 and 12..15 in pairs (XOR 2) gives none.
+__device__ __forceinline__ int kc_swz16(int r) { return (r >> 1) & 2; }
+
 // One global -> LDS copy operand.  CW is the copy width in floats per lane:
 // 4 (16-byte copies; needs 16-byte-aligned rows) or 1 (4-byte copies; any
 // alignment, any K).  Either way the LDS image is the same, so the fragment
@@ -1868,7 +1878,7 @@ sgemm_splitk16_kernel(const float* __restrict__ A0, const float* __restrict__ B0
 // the final sums), so the results are that kernel's bit for bit.
 // LDS images, per wave:
 //  * A: group-major, GR groups of 16 rows x 16 k (one 1 KB copy each); in a
-//    group the 16-byte chunk c of row r sits in slot c ^ kc_swz<4>(r), so a
+//    group the 16-byte chunk c of row r sits in slot c ^ kc_swz16(r), so a
 //    ds_read_b128 of 16 rows x one chunk spreads over the banks.
 //  * B: KC rows of 16 floats, in groups of 16 k; within a group slot row
 //    4s + q holds k = 4q + s, so the ds_read_b32 of MFMA step s (lane quarter
@@ -1959,7 +1969,7 @@ sgemm_splitk16_lds_kernel(const float* __restrict__ A0, const float* __restrict_
         // landed once at most 2 (GR - 1 - g) copies are outstanding.
         const int ar = lane >> 2;             // A: row of this lane's chunk
         const int aq = lane & 3;              // A: slot within the row's group
-        const int ac = aq ^ kc_swz<4>(ar);    // A: the chunk (k / 4 in the group) it holds
+        const int ac = aq ^ kc_swz16(ar);     // A: the chunk (k / 4 in the group) it holds
         const int arow = min(m0 + ar, M - 1) - m0;
         const int sr = lane >> 2;             // B: slot row of the group
         const int kr = 4 * (sr & 3) + (sr >> 2);
@@ -2002,7 +2012,7 @@ sgemm_splitk16_lds_kernel(const float* __restrict__ A0, const float* __restrict_
             if (k0 >= K) return;
             const float* as = region(gc);
             const float* bs = as + 4 * kWave;
-            floatx4 a = *reinterpret_cast<const floatx4*>(as + i * 16 + 4 * (q ^ kc_swz<4>(i)));
+            floatx4 a = *reinterpret_cast<const floatx4*>(as + i * 16 + 4 * (q ^ kc_swz16(i)));
             float b[4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) b[st] = bs[(4 * st + q) * 16 + i];
