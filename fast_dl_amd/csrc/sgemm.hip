@@ -2291,22 +2291,18 @@ sgemm_skinny_part_kernel(const float* __restrict__ A, const float* __restrict__ 
         floatx4 b0[UNR], b1[UNR];
         if (groups > 0) load_b(k, b0);
         // A's slice, all of a thread's loads issued before its first store
-        // (one round trip): TA reads element e = tid + i * 256 as k row e / MR,
-        // column e % MR; otherwise row m = i / R, k = tid + 256 * (i % R).
+        // (one round trip).  Thread tid takes elements e = tid + 256 i of the
+        // LDS image (k row e / MR, column e % MR), so a wave's stores are 64
+        // consecutive floats, free of bank conflicts (with lanes along k they
+        // were MR floats apart: 8-way conflicts at MR = 8).
         const int nrows = k1 - k0;
         constexpr int kThreads = NW * kWave;
-        constexpr int R = kPartMaxRows / kThreads;
-        constexpr int kStagePer = R * MR;
-        static_assert(kPartMaxRows % kThreads == 0, "staging rows in whole passes");
+        constexpr int kStagePer = kPartMaxRows * MR / kThreads;
+        static_assert(kPartMaxRows * MR % kThreads == 0, "staging in whole passes");
         auto stage_pos = [&](int i, int& kk, int& m) {
-            if (TA) {
-                const int e = tid + i * kThreads;
-                kk = e / MR;
-                m = e % MR;
-            } else {
-                m = i / R;
-                kk = tid + (i % R) * kThreads;
-            }
+            const int e = tid + i * kThreads;
+            kk = e / MR;
+            m = e % MR;
         };
         float av[kStagePer];
 #pragma unroll
