@@ -519,11 +519,11 @@ constexpr int kWave = 64;
 // of j is set.  The staging stores (rows j and j + 1 in a half-wave), the z
 // reads (rows j and j + 4), the G2 stores (rows r and r + 4) and the G1 b128
 // reads (16 rows x 4 slots) are then all free of conflicts.  The shift and
-// the swap depend on bit 2 of j alone, so adding a multiple of 8 rows, or 4k
-// rows to a row of the form 4m, or a multiple of 16 columns, moves an address
-// by exactly that many rows and columns: each access below takes a per-lane
-// base plus immediate offsets.  Wider tiles keep a padded row of CM + 4
-// floats, for which the same holds.
+// the swap depend on bit 2 of j alone, so row 4m + s (s < 4) sits s rows
+// from row 4m, and adding a multiple of 8 rows or of 16 columns moves an
+// address by exactly that many rows and columns: each access below takes a
+// per-lane base plus immediate offsets.  Wider tiles keep a padded row of
+// CM + 4 floats, for which the same holds.
 template <int CM>
 __device__ __forceinline__ int head_w2_at(int j, int c) {
     if constexpr (CM == 16) {
